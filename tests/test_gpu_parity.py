@@ -1,0 +1,276 @@
+"""HIP path vs the oracle (and the reference's golden vectors), through the C-ABI library.
+
+Every test runs the kernel on ``cuda:0`` and checks it against the CPU oracle
+on the same seeded inputs: tokens bit-exact (a difference is accepted only
+when the oracle's float64 arithmetic puts it within 1e-5 of a CDF or top-p
+boundary), processed logits bit-exact wherever both are finite, filtered
+probabilities within 1e-5 relative.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from mi355x_sampler import groups as G
+from mi355x_sampler import talker_sampler as hs
+from mi355x_sampler import workloads as W
+from oracle import extended_ref as ext
+from oracle import rng_ref
+from oracle import talker_sampler_ref as ts
+from tests.conftest import golden_case
+from tests.parity import compare_group, oracle_rows, token_at_boundary
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+V, EOS = 6562, 6561
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu(gpu_lib):
+    torch.cuda.set_device(0)
+    yield
+
+
+def run(wl, **kw):
+    d = wl.to(DEV)
+    g = G.RowGroup(d.logits, **d.group_kwargs(), processed=True, probs=True, **kw)
+    G.launch([g])
+    torch.cuda.synchronize()
+    return g
+
+
+WORKLOADS = [
+    ("talker_b1_hf", lambda: W.talker_b1("hf")),
+    ("talker_b1_omni", lambda: W.talker_b1("omni")),
+    ("talker_b8_hf", lambda: W.talker_b8("hf")),
+    ("talker_b8_omni", lambda: W.talker_b8("omni")),
+    ("thinker_b8", lambda: W.thinker_b8()),
+    ("thinker_b8_greedy", lambda: W.thinker_b8(greedy=True)),
+    ("thinker_b64", lambda: W.thinker_b64()),
+]
+
+
+@pytest.mark.parametrize("name,make", WORKLOADS, ids=[n for n, _ in WORKLOADS])
+def test_workload_matches_oracle(name, make):
+    wl = make()
+    print(f"[gpu] workload {name}: rows={wl.rows} vocab={wl.vocab} dtype={wl.logits.dtype}", flush=True)
+    g = run(wl)
+    rows = oracle_rows(wl)
+    ref = ext.sample_rows(rows)
+    stats = compare_group(name, g.tokens, g.processed, g.probs, ref, rows,
+                          prob_rtol=1e-5 if wl.logits.dtype == torch.float32 else 2e-3)
+    print(f"[gpu] {name}: {stats}", flush=True)
+    assert stats["exact"] >= wl.rows - max(1, wl.rows // 16)
+
+
+def test_thinker_greedy_is_first_argmax_at_full_size():
+    wl = W.thinker_b64().to(DEV)
+    x = wl.logits.clone()
+    x[3, 100] = x[3].max()  # a tie: the first index wins
+    x[3, 7] = x[3].max()
+    got = G.greedy(x)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), torch.argmax(x.float().cpu(), dim=-1))
+    x32 = torch.randn(5, W.THINKER_V, device=DEV)
+    assert torch.equal(G.greedy(x32).cpu(), torch.argmax(x32.cpu(), dim=-1))
+
+
+def test_counter_uniform_matches_reference_golden(golden_uniform):
+    g = golden_uniform
+    u = hs.uniform(torch.from_numpy(g["seeds"]).to(DEV), torch.from_numpy(g["steps"]).to(DEV)).cpu().numpy()
+    assert np.array_equal(u.view(np.int32), g["u"].view(np.int32))
+    many = hs.uniform(torch.full((4096,), 9, device=DEV), torch.arange(4096, device=DEV)).cpu().numpy()
+    assert np.array_equal(many, g["many_seed9"])
+
+
+def test_philox_uniform_matches_oracle():
+    rs = np.random.default_rng(2)
+    s = rs.integers(-(2**63), 2**63 - 1, size=2048, dtype=np.int64)
+    t = rs.integers(0, 2**40, size=2048, dtype=np.int64)
+    r = rs.integers(0, 2**20, size=2048, dtype=np.int64)
+    got = hs.philox_uniform(torch.from_numpy(s).to(DEV), torch.from_numpy(t).to(DEV), torch.from_numpy(r).to(DEV))
+    assert np.array_equal(got.cpu().numpy(), rng_ref.philox_uniform(s, t, r))
+
+
+@pytest.mark.parametrize("name", ["hf_b1_t0", "hf_b6_t5", "hf_b6_t60", "omni_b1_t0", "omni_b6_t40", "hf_c1_w64",
+                                  "omni_c1_w64", "hf_c2_w256", "omni_c2_w256"])
+def test_processed_and_draw_match_reference_golden(golden_processed, name):
+    c = golden_case(golden_processed, name)
+    cfg = hs.TalkerSampling(temperature=float(c["temperature"]), top_p=float(c["top_p"]), top_k=int(c["top_k"]),
+                            repetition_penalty=float(c["rep"]), window=int(c["w"]), semantics=str(c["semantics"]),
+                            rng="counter", min_keep=int(c["min_keep"]))
+    logits = torch.from_numpy(c["logits"]).to(DEV)
+    hist = torch.from_numpy(c["history"]).to(DEV)
+    steps = torch.from_numpy(c["steps"]).to(DEV)
+    x = hs.processed_logits(logits, hist, steps, EOS, cfg).cpu()
+    want = torch.from_numpy(c["processed"])
+    if not torch.equal(torch.isinf(x), torch.isinf(want)):
+        pytest.fail(f"{name}: support differs from the reference")  # no boundary case in these fixtures
+    assert np.array_equal(x.numpy().view(np.int32), c["processed"].view(np.int32))
+    tok = hs.draw(torch.from_numpy(c["processed"]).to(DEV), torch.from_numpy(c["seeds"]).to(DEV), steps).cpu()
+    u = rng_ref.counter_uniform(c["seeds"], c["steps"])
+    for i, (a, b) in enumerate(zip(tok.tolist(), c["tokens"].tolist())):
+        assert a == b or token_at_boundary(want[i], float(u[i]), a, b), (name, i, a, b)
+
+
+@pytest.mark.parametrize("name,sem", [("hf", "hf"), ("omni", "omni")])
+def test_decode_streams_match_reference_golden(golden_streams, name, sem):
+    c = golden_case(golden_streams, name)
+    cfg = hs.TalkerSampling(semantics=sem, rng="counter", min_new_tokens=int(c["min_new"]))
+    gen = torch.Generator().manual_seed(int(c["gseed"]))
+    frames, rows = int(c["frames"]), int(c["rows"])
+    logits = torch.randn(frames, rows, V, generator=gen)
+    logits[frames - 10, 1, EOS] = 1e4
+    assert float(logits.double().sum()) == float(c["logits_sum"])
+    st = hs.DecodeState.new([5 + i for i in range(rows)], cfg, device=DEV)
+    toks = hs.decode_k(st, logits.to(DEV), EOS, cfg).cpu().numpy()
+    assert np.array_equal(toks, c["tokens"])
+    assert np.array_equal(st.history.cpu().numpy(), c["history"])
+    assert np.array_equal(st.steps.cpu().numpy(), c["steps"])
+    assert np.array_equal(st.finished.cpu().numpy(), c["finished"])
+
+
+def _boundary_ok(xr, got, want, p, k, full):
+    from tests.parity import support_at_boundary
+    return support_at_boundary(xr, got, want, p, k, full)
+
+
+@pytest.mark.parametrize("scale", [0.3, 1.0, 3.0, 8.0])
+def test_mirror_filters_match_oracle(scale):
+    g = torch.Generator().manual_seed(int(scale * 10))
+    x = torch.randn(16, V, generator=g) * scale
+    xd = x.to(DEV)
+    assert torch.equal(hs.top_k_filter(xd, 25, 3).cpu(), ts.top_k_filter(x, 25, 3))
+    assert torch.equal(hs.top_k_filter(xd, 0, 1).cpu(), ts.top_k_filter(x, 0, 1))
+    for got, want, p, k, full in (
+            (hs.top_k_top_p_filter(xd, 25, 0.85, 1).cpu(), ts.top_k_top_p_filter(x, 25, 0.85, 1), 0.85, 25, False),
+            (hs.top_p_top_k_filter(xd, 0.85, 25, 3).cpu(), ts.top_p_top_k_filter(x, 0.85, 25, 3), 0.85, 25, True),
+            (hs.top_p_filter(xd, 0.9, 1).cpu(), ts.top_p_filter(x, 0.9, 1), 0.9, V, True)):
+        for i in range(x.shape[0]):
+            fin = torch.isfinite(got[i]) & torch.isfinite(want[i])
+            assert torch.equal(got[i][fin], want[i][fin])
+            assert torch.equal(torch.isfinite(got[i]), torch.isfinite(want[i])) or _boundary_ok(
+                x[i], got[i], want[i], p, k, full), (i, scale)
+    hist = torch.randint(0, 300, (16, 64), generator=g)
+    hist[:, :5] = -1
+    assert torch.equal(hs.repetition_penalty(xd, hist.to(DEV), 1.3).cpu(), ts.repetition_penalty(x, hist, 1.3))
+
+
+def test_step_invariants():
+    cfg = hs.TalkerSampling()
+    logits = torch.randn(8, V, device=DEV)
+    alone = hs.step(hs.DecodeState.new([1234], device=DEV), logits[3:4], EOS, cfg)
+    batch = hs.step(hs.DecodeState.new([1, 2, 3, 1234, 5, 6, 7, 8], device=DEV), logits, EOS, cfg)
+    assert int(alone[0]) == int(batch[3])
+    gen = torch.Generator().manual_seed(4)
+    lg = torch.randn(30, 4, V, generator=gen)
+    ref_state = hs.DecodeState.new([1, 2, 3, 4], device=DEV)
+    want = torch.stack([hs.step(ref_state, lg[i].to(DEV), EOS, cfg) for i in range(30)])
+    s = hs.DecodeState.new([1, 2, 3, 4], device=DEV)
+    s.active[2] = False
+    noisy = lg.clone()
+    noisy[:, 2] = torch.randn(30, V, generator=gen) * 100
+    got = torch.stack([hs.step(s, noisy[i].to(DEV), EOS, cfg) for i in range(30)])
+    assert torch.equal(got[:, [0, 1, 3]], want[:, [0, 1, 3]]) and (got[:, 2] == hs.PAD).all()
+    assert int(s.steps[2]) == 0 and (s.history[2] == hs.PAD).all()
+
+
+def test_in_place_step_with_injected_uniforms_equals_step():
+    cfg = hs.TalkerSampling(semantics="omni", rng="counter", min_new_tokens=3)
+    gen = torch.Generator().manual_seed(9)
+    lg = torch.randn(12, 5, V, generator=gen).to(DEV)
+    a = hs.DecodeState.new([11, 12, 13, 14, 15], cfg, device=DEV)
+    b = hs.DecodeState.new([11, 12, 13, 14, 15], cfg, device=DEV)
+    for i in range(12):
+        u = hs.uniform(b.seeds, b.steps)
+        ta = hs.step(a, lg[i], EOS, cfg)
+        tb = hs.step_(b, lg[i], EOS, cfg, uniform_values=u)
+        assert torch.equal(ta, tb)
+    assert torch.equal(a.history, b.history) and torch.equal(a.steps, b.steps)
+
+
+def test_mixed_launch_equals_separate_launches():
+    big, small = W.mixed()
+    bd, sd = big.to(DEV), small.to(DEV)
+    g1 = G.RowGroup(bd.logits, **bd.group_kwargs())
+    g2 = G.RowGroup(sd.logits, **sd.group_kwargs())
+    G.launch([g1, g2])
+    h1 = G.sample(bd.logits, **bd.group_kwargs())
+    h2 = G.sample(sd.logits, **sd.group_kwargs())
+    torch.cuda.synchronize()
+    assert torch.equal(g1.tokens, h1.tokens) and torch.equal(g2.tokens, h2.tokens)
+
+
+@pytest.mark.parametrize("mode", ["window", "ring"])
+def test_state_update_matches_oracle(mode):
+    wl = W.talker_b8("omni", step=0)
+    wl.history[:, :100] = -1
+    rows = oracle_rows(wl)
+    d = wl.to(DEV)
+    hist = d.history.clone()
+    steps = d.steps.clone()
+    finished = torch.zeros(wl.rows, dtype=torch.bool, device=DEV)
+    finished[5] = True
+    rows.finished = finished.cpu().clone()
+    head = torch.arange(wl.rows, dtype=torch.int32, device=DEV) * 7 if mode == "ring" else None
+    head_cpu = head.cpu().to(torch.int64).clone() if head is not None else None
+    kw = d.group_kwargs()
+    kw.update(history=hist, steps=steps, finished=finished, update_state=True, history_head=head)
+    for it in range(5):
+        g = G.sample(d.logits, **kw)
+        ref = ext.sample_rows(rows, update_state=True, history_mode=mode, history_head=head_cpu)
+        torch.cuda.synchronize()
+        assert torch.equal(g.tokens.cpu(), ref["tokens"]), it
+        assert torch.equal(hist.cpu().to(torch.int64), rows.history.to(torch.int64)), it
+        assert torch.equal(steps.cpu(), rows.steps), it
+        if head is not None:
+            assert torch.equal(head.cpu().to(torch.int64), head_cpu % wl.history.shape[1]), it
+
+
+def test_fallback_path_on_clustered_logits():
+    """Top values packed into one slice: the candidates cannot prove the top-k and the row is re-streamed."""
+    wl = W.thinker_b8()
+    x = wl.logits.float()
+    x, _ = torch.sort(x, dim=-1)  # ascending: every top value sits in the last slice
+    wl.logits = x.to(torch.bfloat16)
+    wl.params["top_k"][:] = torch.tensor([1000, 100, 20, 5, 1000, 1, 300, 2], dtype=torch.int32)
+    g = run(wl)
+    rows = oracle_rows(wl)
+    ref = ext.sample_rows(rows)
+    compare_group("fallback", g.tokens, g.processed, g.probs, ref, rows, prob_rtol=2e-3)
+
+
+def test_graph_replay_equals_eager():
+    wl = W.talker_b8("hf").to(DEV)
+    kw = wl.group_kwargs()
+    eager = G.sample(wl.logits, **kw).tokens.clone()
+    torch.cuda.synchronize()
+    grp = G.RowGroup(wl.logits, **kw)
+    G.launch([grp])  # warm the workspace outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        G.launch([grp])  # workspace for this stream
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            G.launch([grp])
+    torch.cuda.synchronize()
+    for _ in range(4):
+        grp.tokens.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(grp.tokens, eager)
+
+
+def test_errors_are_loud():
+    with pytest.raises(ValueError):
+        G.RowGroup(torch.zeros(2, 8))  # CPU tensor: no CPU path
+    with pytest.raises(ValueError):
+        hs.processed_logits(torch.zeros(1, 8, device=DEV), torch.full((1, 2), -1, device=DEV),
+                            torch.zeros(1, dtype=torch.long, device=DEV), 3, hs.TalkerSampling(semantics="x"))
+    with pytest.raises(ValueError):
+        G.sample(torch.zeros(2, 8, device=DEV), eos=9)  # eos outside the vocabulary
