@@ -1,29 +1,38 @@
-// Fused token-sampling kernel for MI355X (gfx950) behind the C-ABI of include/mi355x_sampler.h.
+// Fused token-sampling kernels for MI355X (gfx950) behind the C-ABI of include/mi355x_sampler.h.
 //
-// One launch handles every row of every group.  A row of V logits is cut into
-// S vocabulary slices of at most ~10K elements, one 256-thread workgroup each.
-// A slice workgroup
-//   1. counts its history ids into an LDS table (u16 per slice token),
-//   2. reads its slice once with 16-byte aligned vector loads, applies the
-//      row's pipeline element by element (EOS censor, repetition / frequency /
-//      presence penalties, allowed-token bitmask, temperature, in the order of
-//      engine/talker_sampler.py:142-156) and keeps the values in registers,
-//   3. publishes a summary (max, first argmax, sum of exp relative to its max)
-//      and, for top-k rows, its candidates: every value >= tau, the c-th
-//      largest of the per-thread maxima, in vocabulary order,
+// A row of V logits is cut into S vocabulary slices of at most ~10K elements,
+// one 256-thread workgroup each (XCD-aware: a row's slices share an XCD).
+//
+// sample_kernel, per slice workgroup:
+//   1. counts the row's history ids that fall in the slice into an LDS table,
+//   2. reads the slice once (16-byte vector loads of logits and mask words) and
+//      applies the row's pipeline element by element — EOS censor, repetition /
+//      frequency / presence penalties, allowed-token bitmask, temperature, in
+//      the order of engine/talker_sampler.py:142-156 — keeping the values in
+//      registers,
+//   3. publishes a summary (max, first argmax, sum of exp relative to its max,
+//      per-sub-block sums) and, by row kind, its top-k candidates (every value
+//      >= tau, the c-th largest per-thread maximum, in vocabulary order) or a
+//      probability-mass histogram on a fixed grid of 1/8 logit,
 //   4. increments the row's arrival counter.  The last workgroup to arrive
-//      finalises the row: it merges the summaries, selects the top-k and top-p
-//      thresholds exactly (radix select over order-preserving float keys, by
-//      count and by fixed-point probability mass), draws by inverse CDF in
-//      vocabulary order and updates the decode state in place.
-// The finaliser works on the candidates in LDS when they provably contain the
-// top-k (every value >= max_s tau_s was published and at least k of them are
-// >= it); otherwise (a slice overflowed, the nucleus is not bounded by a
-// top-k, a full-vocabulary draw) it streams the row again slice by slice and
-// runs the same selections over every element.  Workgroups never wait for
-// one another: the only cross-workgroup protocol is release / arrive /
-// acquire on the per-row counter, which the finaliser resets to zero for the
-// next launch.
+//      finalises the row:
+//        greedy rows: first index of the maximum;
+//        top-k rows: sorts the candidate values (bitonic, LDS), reads the
+//          top-k threshold, the top-p cut over the sorted masses and draws by
+//          inverse CDF over the candidates in vocabulary order;
+//        unfiltered rows: walks the sub-block sums to the sub-block holding
+//          u * total and rescans only that sub-block;
+//        top-p-only rows (no top-k): merges the histograms, finds the bin that
+//          holds the top-p boundary and leaves a pending record;
+//        anything the fast paths cannot prove exactly: streams the row again and
+//          selects by radix over order-preserving keys.
+// nucleus_kernel (a small persistent grid over a work list the finalisers built)
+// re-reads only the slices of pending rows, publishes the values inside the
+// boundary bin and the sums of everything above it, and its last workgroup per
+// row resolves the top-p threshold exactly and draws.
+// Workgroups never wait for one another: the only cross-workgroup protocol is
+// release / arrive / acquire on the per-row counter, which the finaliser resets
+// for the next launch.
 
 #include <hip/hip_runtime.h>
 
@@ -34,6 +43,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 
 #include "mi355x_sampler.h"
@@ -42,17 +52,42 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
-constexpr int kNV = 40;            // register slots per thread in the slice phase
+constexpr int kNV = 40;              // register slots per thread in a slice
 constexpr int kMaxGroups = 4;
 constexpr int kMaxSlices = 64;
-constexpr int kCapSlice = 512;     // candidates one slice may publish
-constexpr int kCapRow = 4096;      // candidates the finaliser holds in LDS
+constexpr int kMaxSB = kNV / 4 * kWaves;  // sub-blocks per slice (fp32: 10 rounds x 4 waves)
+constexpr int kCapSlice = 512;       // candidates one slice may publish
+constexpr int kCapRow = 2048;        // candidates the finaliser sorts in LDS
 constexpr int kCntWords = kBlock * kNV / 2;  // two u16 counts per word: covers every element of a slice
-constexpr int kAlphaTable = 256;   // rep**n for n < 256 kept in LDS
-constexpr int kMaxRows = 16384;    // rows per launch (arrival counters live in a fixed prefix of the workspace)
-constexpr int64_t kCounterBytes = 4 * (int64_t)kMaxRows;
+constexpr int kNB = 256;             // histogram bins below a slice's top bin
+constexpr int kAlphaTable = 64;      // rep**n for n < 64 kept in LDS (larger counts take a slow call)
+constexpr float kBinScale = 8.0f;    // bins of 1/8 logit
+constexpr int kMaxRows = 16384;      // rows per launch
+constexpr int kCounterStride = 32;  // u32 words between rows' counters: one 128-byte line each (no atomic contention)
+constexpr int64_t kCounterBytes = 4 * kCounterStride * (int64_t)kMaxRows;
+constexpr int64_t kPendingBytes = 64 * (int64_t)kMaxRows;
+constexpr int64_t kHeaderBytes = 512;                                  // nucleus work-list header
+constexpr int64_t kItemBytes = 4 * (int64_t)kMaxRows * kMaxSlices;     // nucleus work items
+constexpr int kNucleusGrid = 256;                                      // persistent workgroups of the nucleus pass
 constexpr int64_t kPad = -1;
 constexpr double kMassScale = 1099511627776.0;  // 2^40 fixed-point units of exp(x - max)
+
+enum : int32_t { kPendNone = 0, kPendNucleus = 1 };
+
+// Work list of the nucleus pass (each counter on its own 128-byte line); zero between launches.
+struct NucleusHeader {
+    unsigned int n_items;
+    unsigned int pad0[31];
+    unsigned int next;
+    unsigned int pad1[31];
+    unsigned int exited;
+    unsigned int pad2[31];
+};
+static_assert(sizeof(NucleusHeader) <= kHeaderBytes, "header");
+
+__host__ __device__ __forceinline__ unsigned int pack_item(int gi, int row, int slice) {
+    return ((unsigned)gi << 20) | ((unsigned)row << 6) | (unsigned)slice;
+}
 
 struct DevGroup {
     const char* logits;
@@ -97,9 +132,14 @@ struct DevGroup {
     int32_t slices;
     int32_t slice_len;
     int32_t block_begin;
-    int32_t row_begin;      // index of the group's first row among all rows of the launch
-    char* ws;               // the group's row regions
-    unsigned int* counters; // the launch's arrival counters (fixed workspace prefix, all zero between launches)
+    int32_t row_begin;       // index of the group's first row among all rows of the launch
+    char* ws;                // the group's row regions
+    unsigned int* counters;  // arrival counters (fixed workspace prefix, zero between launches)
+    char* pending;           // per-row pending records (fixed workspace region)
+    NucleusHeader* nhdr;     // nucleus work list header and items (fixed workspace region)
+    unsigned int* items;
+    int32_t gi;              // index of this group in the launch
+    int32_t pad2_;
     int64_t ws_row_bytes;
 };
 
@@ -112,44 +152,103 @@ struct KernelArgs {
 };
 
 struct SliceSummary {
-    float m;          // max value of the slice (-inf if none finite)
-    float g;          // the published candidates hold every value >= g (+inf: none published)
-    double z;         // sum of exp(x - m) over the slice
-    int32_t argmax;   // first index of m
+    float m;                 // max value of the slice (-inf if none finite)
+    float g;                 // the published candidates hold every value >= g (+inf: none published)
+    double z;                // sum of exp(x - m) over the slice
+    int32_t argmax;          // first index of m
     int32_t ncand;
     int32_t overflow;
-    int32_t pad_;
+    int32_t hb;              // histogram: top bin floor(8 m)
+    unsigned long long under_q;  // histogram: mass below the window (2^40 units of exp(x - m))
+    int32_t under_n;
+    int32_t n_hi;            // nucleus pass: values above the boundary bin
+    double hi_mass;          // nucleus pass: their sum of exp(x - M)
+    int32_t pad_[2];
 };
+static_assert(sizeof(SliceSummary) == 64, "summary layout");
+
+struct Pending {
+    int32_t mode;
+    float lo_v, hi_v;        // boundary bin [lo_v, hi_v)
+    float m;                 // row max
+    double z;                // full-row sum of exp(x - m)
+    double target;           // top_p * z
+    int32_t pad_[8];
+};
+static_assert(sizeof(Pending) == 64, "pending layout");
 
 struct Cand {
     float f;
     int32_t j;
 };
 
+// Row workspace: [S summaries][S x kMaxSB sub-block sums][S x kNB bin counts][S x kNB bin masses][S x kCapSlice cands]
+struct RowWs {
+    SliceSummary* summ;
+    double* sb;
+    uint32_t* hcnt;
+    unsigned long long* hmass;
+    Cand* cand;
+};
+
+__host__ __device__ __forceinline__ int64_t row_ws_bytes(int s) {
+    const int64_t b = (int64_t)s * (sizeof(SliceSummary) + 8 * kMaxSB + 12 * kNB + sizeof(Cand) * kCapSlice);
+    return (b + 255) & ~(int64_t)255;
+}
+
+__device__ __forceinline__ RowWs row_ws(char* base, int s) {
+    RowWs w;
+    w.summ = (SliceSummary*)base;
+    w.sb = (double*)(base + (int64_t)s * sizeof(SliceSummary));
+    w.hcnt = (uint32_t*)((char*)w.sb + (int64_t)s * 8 * kMaxSB);
+    w.hmass = (unsigned long long*)((char*)w.hcnt + (int64_t)s * 4 * kNB);
+    w.cand = (Cand*)((char*)w.hmass + (int64_t)s * 8 * kNB);
+    return w;
+}
+
+// The penalty of an element seen n times: x < 0 ? x * a : x / a, minus freq * n, minus pres (n > 0), with
+// a = rep**n.  Entry 0 is the identity.  ra = RN(1 / a) serves the corrected-reciprocal division.
+struct PenEntry {
+    float a, ra, fn, pn;
+};
+
+// Allowed-bit words of a slice in LDS: word k covers elements [32 * (wb + k), +32) with wb = first >> 5.
+constexpr int kMaskWords = kBlock * kNV / 32 + 2;
+
 struct Smem {
-    union {
-        uint32_t cnt[kCntWords];  // slice phase and streaming: history counts (u16 pairs)
+    union alignas(16) {
+        uint32_t cnt[kCntWords];  // history counts of a slice (u16 pairs)
         struct {
             float val[kCapRow];   // finaliser: candidate values, vocabulary order
-            int32_t id[kCapRow];
-        } cand;
+            int32_t id[kCapRow];  //            their ids
+            uint32_t key[kCapRow];  //          order keys, sorted descending
+        } c;
+        double sbs[kMaxSlices * kMaxSB];  // finaliser: sub-block totals
+        struct {
+            double mass[kNB];
+            uint32_t cnt[kNB];
+        } h;
     } u;
-    float alpha[kAlphaTable];
     float tmax[kBlock];
-    uint32_t hcnt[256];
-    unsigned long long hmass[256];
+    uint32_t hcnt[kNB];
+    unsigned long long hmass[kNB];
+    double sbw[kMaxSB];
+    PenEntry pen[kAlphaTable];
+    uint32_t mask[kMaskWords];
     double red_d[kWaves];
     unsigned long long red_u[kWaves];
     float red_f[kWaves];
     int32_t red_i[kWaves];
     double tile_sum[kMaxSlices];
     SliceSummary summ[kMaxSlices];
+    Cand stage[kCapSlice];  // a slice's published candidates, copied out by wave 0
     int32_t sel_bin;
     int32_t sel_rem;
     int32_t is_last;
     int32_t pad_;
     unsigned long long sel_acc;
     float sel_tau;
+    unsigned int item;
 };
 
 __device__ __forceinline__ uint32_t ord_key(float f) {
@@ -162,6 +261,65 @@ __device__ __forceinline__ float key_float(uint32_t k) {
 }
 
 __device__ __forceinline__ bool finite_f(float f) { return f > -INFINITY && f < INFINITY; }
+
+__device__ __forceinline__ int bin_of(float f) {
+    return (int)floorf(fminf(fmaxf(f * kBinScale, -1.0e9f), 1.0e9f));
+}
+
+// ---------------------------------------------------------------- cross-workgroup publication
+// Data one workgroup publishes for another (summaries, sums, histograms, candidates) is written and read with
+// relaxed device-scope atomic stores and loads, which are coherent across XCDs without writing back or
+// invalidating whole caches; the publisher orders them before its arrival count by waiting for its stores.
+
+template <class T>
+__device__ __forceinline__ void pub_st(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class T>
+__device__ __forceinline__ T pub_ld(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void pub_st_cand(Cand* p, Cand v) {
+    pub_st((unsigned long long*)p, ((unsigned long long)(uint32_t)v.j << 32) | __float_as_uint(v.f));
+}
+
+__device__ __forceinline__ Cand pub_ld_cand(const Cand* p) {
+    const unsigned long long w = pub_ld((const unsigned long long*)p);
+    return Cand{__uint_as_float((uint32_t)w), (int32_t)(uint32_t)(w >> 32)};
+}
+
+__device__ __forceinline__ void pub_st_summary(SliceSummary* d, const SliceSummary& v) {
+    pub_st(&d->m, v.m);
+    pub_st(&d->g, v.g);
+    pub_st(&d->z, v.z);
+    pub_st(&d->argmax, v.argmax);
+    pub_st(&d->ncand, v.ncand);
+    pub_st(&d->overflow, v.overflow);
+    pub_st(&d->hb, v.hb);
+    pub_st(&d->under_q, v.under_q);
+    pub_st(&d->under_n, v.under_n);
+    pub_st(&d->n_hi, v.n_hi);
+    pub_st(&d->hi_mass, v.hi_mass);
+}
+
+__device__ __forceinline__ SliceSummary pub_ld_summary(const SliceSummary* d) {
+    SliceSummary v;
+    v.m = pub_ld(&d->m);
+    v.g = pub_ld(&d->g);
+    v.z = pub_ld(&d->z);
+    v.argmax = pub_ld(&d->argmax);
+    v.ncand = pub_ld(&d->ncand);
+    v.overflow = pub_ld(&d->overflow);
+    v.hb = pub_ld(&d->hb);
+    v.under_q = pub_ld(&d->under_q);
+    v.under_n = pub_ld(&d->under_n);
+    v.n_hi = pub_ld(&d->n_hi);
+    v.hi_mass = pub_ld(&d->hi_mass);
+    v.pad_[0] = v.pad_[1] = 0;
+    return v;
+}
 
 // ---------------------------------------------------------------- block primitives (every thread calls them)
 
@@ -188,6 +346,16 @@ __device__ __forceinline__ int block_min_i(int x, Smem& sm) {
     return r;
 }
 
+__device__ __forceinline__ int block_max_i(int x, Smem& sm) {
+    for (int o = 32; o; o >>= 1) x = max(x, __shfl_xor(x, o));
+    __syncthreads();
+    if (lane_id() == 0) sm.red_i[wave_id()] = x;
+    __syncthreads();
+    int r = sm.red_i[0];
+    for (int i = 1; i < kWaves; ++i) r = max(r, sm.red_i[i]);
+    return r;
+}
+
 __device__ __forceinline__ int block_sum_i(int x, Smem& sm) {
     for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
     __syncthreads();
@@ -207,6 +375,21 @@ __device__ __forceinline__ double block_sum_d(double x, Smem& sm) {
     double r = 0.0;
     for (int i = 0; i < kWaves; ++i) r += sm.red_d[i];
     return r;
+}
+
+__device__ __forceinline__ unsigned long long block_sum_u(unsigned long long x, Smem& sm) {
+    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    __syncthreads();
+    if (lane_id() == 0) sm.red_u[wave_id()] = x;
+    __syncthreads();
+    unsigned long long r = 0;
+    for (int i = 0; i < kWaves; ++i) r += sm.red_u[i];
+    return r;
+}
+
+__device__ __forceinline__ double wave_sum_d(double x) {
+    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    return x;
 }
 
 // Exclusive prefix from the lane-shifted inclusive scan (no subtraction).
@@ -230,20 +413,21 @@ __device__ __forceinline__ double block_excl_scan_d(double x, double& total, Sme
     return off + excl;
 }
 
-__device__ __forceinline__ int block_excl_scan_i(int x, int& total, Smem& sm) {
-    int incl = x;
+__device__ __forceinline__ unsigned long long block_excl_scan_u(unsigned long long x, unsigned long long& total,
+                                                               Smem& sm) {
+    unsigned long long incl = x;
     for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o);
+        const unsigned long long y = __shfl_up(incl, o);
         if (lane_id() >= o) incl += y;
     }
     __syncthreads();
-    if (lane_id() == 63) sm.red_i[wave_id()] = incl;
+    if (lane_id() == 63) sm.red_u[wave_id()] = incl;
     __syncthreads();
-    int off = 0;
+    unsigned long long off = 0;
     total = 0;
     for (int i = 0; i < kWaves; ++i) {
-        if (i < wave_id()) off += sm.red_i[i];
-        total += sm.red_i[i];
+        if (i < wave_id()) off += sm.red_u[i];
+        total += sm.red_u[i];
     }
     return off + incl - x;
 }
@@ -251,23 +435,27 @@ __device__ __forceinline__ int block_excl_scan_i(int x, int& total, Smem& sm) {
 // ---------------------------------------------------------------- per-row context
 
 struct Ctx {
-    int row, slice, S, V, slice_len;
+    int row, slice, S, V, slice_len, grow;  // grow: row index among all rows of the launch
     int64_t step;
     float tdiv;        // temperature divisor (1 for greedy rows)
+    float rtdiv;       // RN(1 / tdiv)
     float top_p;
     float rep, pres, freq;
     int k_eff;
     int min_keep_eff;  // min(min_keep, k_eff)
     bool greedy, hf, later, censor, forced, live, want_out, p_active;
     bool counts;       // history penalties apply: build the count table
-    bool cand_mode;    // slices publish candidates
     bool full_draw;    // no filter: every finite value survives
+    bool cand_mode;    // top-k bounded: slices publish candidates
+    bool nucleus;      // top-p without top-k: slices publish mass histograms, second pass resolves
+    bool need_mass;    // slices publish exp sums (full-vocabulary normaliser, sub-block sums)
     int cand_target;   // per-slice candidate count target
 };
 
 __device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, Ctx& c) {
     c.row = row;
     c.slice = slice;
+    c.grow = G.row_begin + row;
     c.S = G.slices;
     c.V = G.vocab;
     c.slice_len = G.slice_len;
@@ -275,6 +463,7 @@ __device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, 
     const float t = G.temperature ? G.temperature[row] : G.t_val;
     c.greedy = !(t > 0.f);
     c.tdiv = c.greedy ? 1.0f : t;
+    c.rtdiv = 1.0f / c.tdiv;
     c.top_p = G.top_p ? G.top_p[row] : G.p_val;
     c.rep = G.repetition ? G.repetition[row] : G.rep_val;
     c.pres = G.presence ? G.presence[row] : G.pres_val;
@@ -299,16 +488,19 @@ __device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, 
     c.counts = pen && (!c.hf || c.later);
     const bool filters = !c.greedy && (!c.hf || c.later);
     c.full_draw = !c.greedy && (!filters || (c.k_eff >= c.V && !c.p_active));
-    const int per_slice = (5 * c.k_eff + 4 * c.S - 1) / (4 * c.S) + 8;  // 1.25 k / S + 8
+    const int per_slice = (11 * c.k_eff + 10 * c.S - 1) / (10 * c.S) + 8;  // 1.1 k / S + 8
     c.cand_target = min(per_slice, kBlock);
     c.cand_mode = filters && !c.full_draw && per_slice <= kBlock && c.k_eff <= kCapRow / 2;
+    c.nucleus = filters && !c.full_draw && !c.cand_mode && c.k_eff >= c.V && c.p_active;
+    c.need_mass = c.full_draw || c.nucleus || (c.hf && filters && c.p_active);
 }
 
 // ---------------------------------------------------------------- the element pipeline
 
-// rep**n beyond the LDS table: binary powering in double (<= 32 products, relative error < 4e-15),
-// rounded once to float.
-__device__ __noinline__ float alpha_slow(float rep, int n) {
+// rep**n by binary powering in double (<= 32 products, relative error < 4e-15) rounded once to float, or the
+// caller's table where it covers n.
+__device__ __forceinline__ float alpha_exact(const DevGroup& G, float rep, int n) {
+    if (G.alpha_lut != nullptr && n < G.alpha_lut_len) return G.alpha_lut[n];
     double r = 1.0, b = (double)rep;
     for (unsigned e = (unsigned)n; e; e >>= 1) {
         if (e & 1u) r *= b;
@@ -317,48 +509,135 @@ __device__ __noinline__ float alpha_slow(float rep, int n) {
     return (float)r;
 }
 
-__device__ __forceinline__ float penalize(float x, int n, const Ctx& c, const Smem& sm) {
-    const float a = n < kAlphaTable ? sm.alpha[n] : alpha_slow(c.rep, n);
-    x = (x < 0.f) ? x * a : x / a;
-    x = x - c.freq * (float)n;  // built with -ffp-contract=off: product and difference round separately
-    return x - c.pres;
+__device__ __forceinline__ PenEntry pen_entry(const DevGroup& G, const Ctx& c, int n) {
+    PenEntry e;
+    if (n == 0) {
+        e.a = 1.0f;
+        e.ra = 1.0f;
+        e.fn = 0.0f;
+        e.pn = 0.0f;
+    } else {
+        e.a = alpha_exact(G, c.rep, n);
+        e.ra = 1.0f / e.a;
+        e.fn = c.freq * (float)n;  // built with -ffp-contract=off: product and difference round separately
+        e.pn = c.pres;
+    }
+    return e;
+}
+
+// x / d rounded to nearest from r = RN(1/d): each step computes the residual x - q*d exactly with one fma and
+// corrects q by it; the first makes q faithful, the second rounds it correctly (Markstein).  The residual is
+// formed as q*d - x so a zero x keeps its sign.  Exact (checked against IEEE division) for
+// 2^-64 <= |x| <= 2^64 and 2^-16 <= d <= 2^16; callers send other x (zero, infinite, NaN, extreme) to IEEE
+// division.
+__device__ __forceinline__ float div_rn(float x, float d, float r) {
+    float q = x * r;
+    float e = fmaf(q, d, -x);
+    q = fmaf(-e, r, q);
+    e = fmaf(q, d, -x);
+    return fmaf(-e, r, q);
+}
+
+__device__ __forceinline__ bool div_in_range(float x) {
+    return (__float_as_uint(x) & 0x7fffffffu) - 0x1f800000u < 0x40000000u;  // 2^-64 <= |x| < 2^64
+}
+
+__device__ __forceinline__ bool divisor_in_range(float d) { return d >= 0x1p-16f && d <= 0x1p16f; }
+
+__device__ __forceinline__ float pen_exact(float x, const PenEntry& e) {
+    x = x < 0.f ? x * e.a : x / e.a;
+    x = x - e.fn;
+    return x - e.pn;
+}
+
+__device__ __forceinline__ float penalize(float x, int n, const DevGroup& G, const Ctx& c, const Smem& sm) {
+    return pen_exact(x, n < kAlphaTable ? sm.pen[n] : pen_entry(G, c, n));
 }
 
 __device__ __forceinline__ float transform(float x, int j, int n, bool allowed, const DevGroup& G, const Ctx& c,
                                            const Smem& sm) {
     if (c.hf) {
         x = x / c.tdiv;
-        if (n > 0) x = penalize(x, n, c, sm);
+        if (n > 0) x = penalize(x, n, G, c, sm);
         if (!allowed) x = -INFINITY;
     } else {
         if (c.censor && j == G.eos) x = -INFINITY;
-        if (n > 0) x = penalize(x, n, c, sm);
+        if (n > 0) x = penalize(x, n, G, c, sm);
         if (!allowed) x = -INFINITY;
         x = x / c.tdiv;
     }
     return x;
 }
 
-// History counts of the slice [lo, hi) into sm.u.cnt (u16 pairs) and the alpha table.  History entries < 0
-// (PAD) or >= V are empty slots.
-__device__ __forceinline__ void build_counts(const DevGroup& G, const Ctx& c, int lo, int hi, Smem& sm) {
-    __syncthreads();  // the union may still be read by a previous pass
-    for (int w = threadIdx.x; w < kCntWords; w += kBlock) sm.u.cnt[w] = 0u;
-    if (threadIdx.x < kAlphaTable) {
-        const int n = threadIdx.x;
-        sm.alpha[n] = (G.alpha_lut != nullptr && n < G.alpha_lut_len) ? G.alpha_lut[n]
-                                                                         : (float)pow((double)c.rep, (double)n);
+// History counts of the elements [lo, hi) into sm.u.cnt as u16 pairs, element j at slot j - base (base <= lo;
+// words [0, words) are cleared first), and the penalty table into sm.pen.  Entries < 0 (PAD) or >= V are empty.
+// The history is loaded before the table is cleared, so the loads overlap the clearing barrier.  Ends with a
+// barrier; returns nonzero (in every thread) when a table entry's rep**n lies outside [2^-16, 2^16].
+__device__ __forceinline__ void count_id(Smem& sm, int64_t h, int base, int lo, int hi) {
+    if (h >= lo && h < hi) {
+        const int s = (int)(h - base);
+        atomicAdd(&sm.u.cnt[s >> 1], 1u << (16 * (s & 1)));
     }
-    __syncthreads();
+}
+
+__device__ __forceinline__ int clear_counts(const DevGroup& G, const Ctx& c, int words, Smem& sm) {
+    __syncthreads();  // the union may still be in use
+    for (int w = threadIdx.x; w < words; w += kBlock) sm.u.cnt[w] = 0u;
+    int bad = 0;
+    if (threadIdx.x < kAlphaTable) {
+        const PenEntry e = pen_entry(G, c, threadIdx.x);
+        sm.pen[threadIdx.x] = e;
+        bad = !divisor_in_range(e.a);
+    }
+    return bad;
+}
+
+__device__ __forceinline__ int build_counts(const DevGroup& G, const Ctx& c, int base, int lo, int hi, int words,
+                                            Smem& sm) {
     const char* hrow = G.history + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
-    for (int i = threadIdx.x; i < G.hist_len; i += kBlock) {
-        const int64_t h = G.hist_i64 ? ((const int64_t*)hrow)[i] : (int64_t)((const int32_t*)hrow)[i];
-        if (h >= lo && h < hi) {
-            const int s = (int)(h - lo);
-            atomicAdd(&sm.u.cnt[s >> 1], 1u << (16 * (s & 1)));
+    const int W = G.hist_len;
+    const bool vec = !G.hist_i64 && (((uintptr_t)hrow) & 15) == 0 && (W & 3) == 0;
+    int bad = 0;
+    if (vec) {
+        const int4* h4 = (const int4*)hrow;
+        const int nv = W >> 2;
+        for (int b0 = 0; b0 < nv || b0 == 0; b0 += kBlock * 4) {
+            int4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = b0 + u * kBlock + threadIdx.x;
+                v[u] = i < nv ? h4[i] : make_int4(-1, -1, -1, -1);
+            }
+            if (b0 == 0) {
+                bad = clear_counts(G, c, words, sm);
+                __syncthreads();
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                count_id(sm, v[u].x, base, lo, hi);
+                count_id(sm, v[u].y, base, lo, hi);
+                count_id(sm, v[u].z, base, lo, hi);
+                count_id(sm, v[u].w, base, lo, hi);
+            }
+        }
+    } else {
+        for (int b0 = 0; b0 < W || b0 == 0; b0 += kBlock * 8) {
+            int64_t h[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = b0 + u * kBlock + threadIdx.x;
+                h[u] = i < W ? (G.hist_i64 ? ((const int64_t*)hrow)[i] : (int64_t)((const int32_t*)hrow)[i])
+                             : (int64_t)-1;
+            }
+            if (b0 == 0) {
+                bad = clear_counts(G, c, words, sm);
+                __syncthreads();
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) count_id(sm, h[u], base, lo, hi);
         }
     }
-    __syncthreads();
+    return __syncthreads_or(bad);
 }
 
 __device__ __forceinline__ int count_of(const Smem& sm, int slot) {
@@ -388,50 +667,220 @@ __device__ __forceinline__ Geo slice_geo(const DevGroup& G, const Ctx& c, int s)
 
 template <int ES>
 __device__ __forceinline__ float raw_elem(const uint4& r, int e) {
-    const uint32_t w = (e >> (ES == 2 ? 1 : 0)) == 0 ? r.x : (e >> (ES == 2 ? 1 : 0)) == 1 ? r.y
-                       : (e >> (ES == 2 ? 1 : 0)) == 2 ? r.z : r.w;
-    if (ES == 2) return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
-    return __uint_as_float(w);
+    const int w = ES == 2 ? (e >> 1) : e;
+    const uint32_t v = w == 0 ? r.x : w == 1 ? r.y : w == 2 ? r.z : r.w;
+    if (ES == 2) return __uint_as_float((e & 1) ? (v & 0xffff0000u) : (v << 16));
+    return __uint_as_float(v);
 }
 
-// Processed value of element j (in [lo, hi)) from its raw logit.
-__device__ __forceinline__ float element(const DevGroup& G, const Ctx& c, const Smem& sm, const uint32_t* mrow, int lo,
-                                         int j, float x) {
-    const int n = c.counts ? count_of(sm, j - lo) : 0;
-    const bool allowed = mrow ? ((mrow[j >> 5] >> (j & 31)) & 1u) != 0u : true;
-    return transform(x, j, n, allowed, G, c, sm);
+// The allowed-mask words covering chunk elements [j0, j0 + E): word of max(j0, 0) and the next one.
+struct MaskPair {
+    uint32_t w0, w1;
+    int base;  // word index of w0
+};
+
+__device__ __forceinline__ MaskPair mask_pair(const uint32_t* mrow, int nwords, int j0) {
+    MaskPair p;
+    p.base = max(j0, 0) >> 5;
+    p.w0 = p.base < nwords ? mrow[p.base] : 0u;
+    p.w1 = p.base + 1 < nwords ? mrow[p.base + 1] : 0u;
+    return p;
+}
+
+__device__ __forceinline__ bool mask_bit(const MaskPair& p, int j) {
+    const uint32_t w = (j >> 5) == p.base ? p.w0 : p.w1;
+    return ((w >> (j & 31)) & 1u) != 0u;
 }
 
 // ---------------------------------------------------------------- slice phase: the slice in registers
 
+// A slice's processed values in registers: thread t holds chunks t + kBlock * i (16 bytes each) in slots
+// [E * i, E * i + E).  Elements outside the slice (the aligned chunks' overhang) hold -inf.
 struct Tile {
     float v[kNV];
-    unsigned long long valid;
+};
+
+// Raw 16-byte chunks of a slice, loaded into registers before the prologue so the loads overlap it.
+template <int ES>
+struct RawTile {
+    uint4 r[kNV / (16 / ES)];
 };
 
 template <int ES>
-__device__ __forceinline__ void load_tile(const DevGroup& G, const Ctx& c, const Geo& g, Tile& T, const Smem& sm) {
+__device__ __forceinline__ void issue_tile(const Geo& g, RawTile<ES>& R) {
+    constexpr int NCH = kNV / (16 / ES);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const int ch = threadIdx.x + kBlock * i;
+        R.r[i] = ch < g.nchunk ? *(const uint4*)(g.base + (uintptr_t)ch * 16) : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
+// The slice's allowed bits into sm.mask: an element is allowed when it lies in [lo, hi), the row's bitmask (if
+// any) allows it, and (omni order) it is not the censored EOS.  With the row's counts (sm.u.cnt, slot j - first)
+// and penalty table when its penalties apply.  Ends with a barrier; returns nonzero when the table holds an
+// alpha outside the corrected-reciprocal range.
+__device__ __forceinline__ int slice_prologue(const DevGroup& G, const Ctx& c, const Geo& g, int E, Smem& sm) {
+    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+    const int wb = g.first >> 5;  // arithmetic shift: first may be negative in slice 0
+    const int eos = (!c.hf && c.censor) ? G.eos : -1;
+    uint32_t mw[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int gw = wb + (int)threadIdx.x + u * kBlock;
+        const int a = g.lo - 32 * gw, b = g.hi - 32 * gw;
+        uint32_t m = (a <= 0 ? ~0u : a >= 32 ? 0u : ~0u << a) & (b >= 32 ? ~0u : b <= 0 ? 0u : (1u << b) - 1u);
+        if (m != 0u && mrow != nullptr) m &= mrow[gw];  // m != 0: word gw meets [lo, hi), inside the row
+        if (eos >= 0 && (eos >> 5) == gw) m &= ~(1u << (eos & 31));
+        mw[u] = m;
+    }
+    int pen_bad = 0;
+    if (c.counts)
+        pen_bad = build_counts(G, c, g.first, g.lo, g.hi, g.nchunk * E / 2, sm);  // ends with a barrier
+    else
+        __syncthreads();  // the previous use of sm.mask is over
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = threadIdx.x + u * kBlock;
+        if (i < kMaskWords) sm.mask[i] = mw[u];
+    }
+    __syncthreads();
+    return pen_bad;
+}
+
+// Division by the temperature: IEEE, corrected reciprocal, or (power-of-two divisor) one exact product.
+enum DivMode { kDivIeee = 0, kDivFast = 1, kDivPow2 = 2 };
+
+// One element of the row's pipeline with IEEE division, for the chunks the fast form does not cover.
+template <bool HF, bool COUNTS>
+__device__ __forceinline__ float elem_ieee(float x, int n, const DevGroup& G, const Ctx& c, const Smem& sm) {
+    if (HF) x = x / c.tdiv;
+    if (COUNTS) x = pen_exact(x, n < kAlphaTable ? sm.pen[n] : pen_entry(G, c, n));
+    if (!HF) x = x / c.tdiv;
+    return x;
+}
+
+// The row's pipeline on one tile.  HF: temperature, then penalties (engine/talker_sampler.py:149-154);
+// otherwise penalties, then temperature (:145-146).  Masked, censored and out-of-slice elements become -inf
+// at the end (-inf is absorbing under both orders).  Per chunk: one LDS read of its allowed bits, one of its
+// counts; a chunk holding a count >= kAlphaTable or a division operand outside div_rn's range is recomputed
+// with IEEE division.
+template <int ES, bool HF, bool COUNTS, int DIV>
+__device__ __forceinline__ void process_tile_t(const DevGroup& G, const Ctx& c, const Geo& g, const RawTile<ES>& R,
+                                               Tile& T, const Smem& sm) {
     constexpr int E = 16 / ES;
     constexpr int NCH = kNV / E;
-    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
-    T.valid = 0ull;
-    uint4 raw[NCH];
+    const float d = c.tdiv, rd = c.rtdiv;
+    const int wb = g.first >> 5;
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
         const int ch = threadIdx.x + kBlock * i;
-        raw[i] = ch < g.nchunk ? *(const uint4*)(g.base + (uintptr_t)ch * 16) : make_uint4(0u, 0u, 0u, 0u);
-    }
+        const int j0 = g.first + ch * E;
+        const bool live = ch < g.nchunk;
+        const int k = min((j0 >> 5) - wb, kMaskWords - 2);
+        const uint32_t bits = live ? __builtin_amdgcn_alignbit(sm.mask[k + 1], sm.mask[k], (uint32_t)(j0 & 31)) : 0u;
+        uint32_t cw[E / 2];
+        bool slow = false;
+        if (COUNTS) {
+            if (ES == 2) {
+                const uint4 v = *(const uint4*)&sm.u.cnt[ch * 4];
+                cw[0] = v.x;
+                cw[1] = v.y;
+                cw[2] = v.z;
+                cw[3] = v.w;
+            } else {
+                const uint2 v = *(const uint2*)&sm.u.cnt[ch * 2];
+                cw[0] = v.x;
+                cw[1] = v.y;
+            }
+            uint32_t any = 0u;
 #pragma unroll
-    for (int i = 0; i < NCH; ++i) {
-        const int ch = threadIdx.x + kBlock * i;
+            for (int w = 0; w < E / 2; ++w) {
+                cw[w] = live ? cw[w] : 0u;
+                any |= cw[w];
+            }
+            slow = (any & 0xffc0ffc0u) != 0u;  // some count >= 64
+        }
+        float f[E];
 #pragma unroll
         for (int e = 0; e < E; ++e) {
-            const int q = i * E + e;
-            const int j = g.first + ch * E + e;
-            const bool in = ch < g.nchunk && j >= g.lo && j < g.hi;
-            T.v[q] = in ? element(G, c, sm, mrow, g.lo, j, raw_elem<ES>(raw[i], e)) : -INFINITY;
-            if (in) T.valid |= 1ull << q;
+            const float x = raw_elem<ES>(R.r[i], e);
+            const int n = COUNTS ? (int)((cw[e >> 1] >> (16 * (e & 1))) & 63u) : 0;
+            if (DIV == kDivIeee) {
+                f[e] = elem_ieee<HF, COUNTS>(x, n, G, c, sm);
+                continue;
+            }
+            float y = x;
+            if (HF) {
+                if (DIV == kDivPow2) {
+                    y = y * rd;
+                } else {
+                    slow |= !div_in_range(y);
+                    y = div_rn(y, d, rd);
+                }
+            }
+            if (COUNTS) {
+                const PenEntry pe = sm.pen[n];
+                slow |= !(y < 0.f) && !div_in_range(y) && y != 0.f;
+                const float q = div_rn(y, pe.a, pe.ra);
+                y = y < 0.f ? y * pe.a : q;
+                y = (y - pe.fn) - pe.pn;
+            }
+            if (!HF) {
+                if (DIV == kDivPow2) {
+                    y = y * rd;
+                } else {
+                    slow |= !div_in_range(y);
+                    y = div_rn(y, d, rd);
+                }
+            }
+            f[e] = y;
         }
+        if (DIV != kDivIeee || COUNTS) {
+            if (slow) {
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int n = COUNTS ? (int)((cw[e >> 1] >> (16 * (e & 1))) & 0xffffu) : 0;
+                    f[e] = elem_ieee<HF, COUNTS>(raw_elem<ES>(R.r[i], e), n, G, c, sm);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < E; ++e) T.v[i * E + e] = ((bits >> e) & 1u) ? f[e] : -INFINITY;
+    }
+}
+
+template <int ES, bool HF, bool COUNTS>
+__device__ __forceinline__ void process_tile_d(const DevGroup& G, const Ctx& c, const Geo& g, const RawTile<ES>& R,
+                                               Tile& T, const Smem& sm, int mode) {
+    if (mode == kDivPow2)
+        process_tile_t<ES, HF, COUNTS, kDivPow2>(G, c, g, R, T, sm);
+    else if (mode == kDivFast)
+        process_tile_t<ES, HF, COUNTS, kDivFast>(G, c, g, R, T, sm);
+    else
+        process_tile_t<ES, HF, COUNTS, kDivIeee>(G, c, g, R, T, sm);
+}
+
+template <int ES>
+__device__ __forceinline__ void load_tile(const DevGroup& G, const Ctx& c, const Geo& g, Tile& T, Smem& sm) {
+    constexpr int E = 16 / ES;
+    RawTile<ES> R;
+    issue_tile<ES>(g, R);
+    const int pen_bad = slice_prologue(G, c, g, E, sm);
+    // pow2: d = 2^k, so x * 2^-k is x / d correctly rounded for every x
+    const bool pow2 = (__float_as_uint(c.tdiv) & 0x807fffffu) == 0u && c.tdiv >= 0x1p-126f && c.tdiv <= 0x1p126f;
+    int mode = pow2 ? kDivPow2 : divisor_in_range(c.tdiv) ? kDivFast : kDivIeee;
+    if (c.counts && pen_bad) mode = kDivIeee;
+    if (c.hf) {
+        if (c.counts)
+            process_tile_d<ES, true, true>(G, c, g, R, T, sm, mode);
+        else
+            process_tile_d<ES, true, false>(G, c, g, R, T, sm, mode);
+    } else {
+        if (c.counts)
+            process_tile_d<ES, false, true>(G, c, g, R, T, sm, mode);
+        else
+            process_tile_d<ES, false, false>(G, c, g, R, T, sm, mode);
     }
 }
 
@@ -441,40 +890,118 @@ __device__ __forceinline__ int tile_index(const Geo& g, int q) {
     return g.first + (int)(threadIdx.x + kBlock * (q / E)) * E + (q % E);
 }
 
-// ---------------------------------------------------------------- finaliser sources
+// Sub-block of element j of slice s: (round, wave) of the slice's chunk layout; a sub-block is 64 consecutive
+// chunks, i.e. a contiguous vocabulary range.
+template <int ES>
+__device__ __forceinline__ int sub_block_of(const Geo& g, int j) {
+    constexpr int E = 16 / ES;
+    const int ch = (j - g.first) / E;
+    return (ch / kBlock) * kWaves + (ch % kBlock) / 64;
+}
 
-// The elements the finaliser selects from: the LDS candidates (n of them, vocabulary order) or the whole row,
-// streamed slice by slice from global memory.
-struct Src {
-    bool cand;
-    int n;
-};
+// Per-(round, wave) sums of exp(v - ref) over the tile's finite values with v >= floor_v; lane 0 of each wave
+// stores them to sm.sbw.  Returns the thread's total.
+template <int ES>
+__device__ __forceinline__ double tile_sub_sums(const Tile& T, float ref, float floor_v, Smem& sm) {
+    constexpr int E = 16 / ES;
+    constexpr int NCH = kNV / E;
+    double tot = 0.0;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        double part = 0.0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int q = i * E + e;
+            const float f = T.v[q];
+            if (f >= floor_v && finite_f(f)) part += (double)expf(f - ref);
+        }
+        tot += part;
+        const double w = wave_sum_d(part);
+        if (lane_id() == 0) sm.sbw[i * kWaves + wave_id()] = w;
+    }
+    return tot;
+}
 
-// Streams slice s: fn(f, j, round, e) for every element, chunk ch = round * kBlock + thread.  Every thread runs
-// the same number of rounds (so fn may not synchronise, but callers may between slices).
+// Publishes the tile's values with lo_v <= v < hi_v (finite) in vocabulary order into cands (at most kCapSlice),
+// staged in LDS and written out by wave 0 (so that wave's device-scope release covers them).  Returns the number
+// found (may exceed kCapSlice).
+template <int ES>
+__device__ __forceinline__ int publish_range(const Tile& T, const Geo& geo, float lo_v, float hi_v, Cand* cands,
+                                             Smem& sm) {
+    constexpr int E = 16 / ES;
+    constexpr int NCH = kNV / E;
+    static_assert(NCH <= 10, "packed scan holds 5 rounds per word");
+    // counts per round, packed 12 bits per round, 5 rounds per 64-bit word: one scan per word
+    unsigned long long pk0 = 0ull, pk1 = 0ull;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        unsigned long long mine = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int q = i * E + e;
+            const float f = T.v[q];
+            if (finite_f(f) && f >= lo_v && f < hi_v) ++mine;
+        }
+        if (i < 5)
+            pk0 |= mine << (12 * i);
+        else
+            pk1 |= mine << (12 * (i - 5));
+    }
+    unsigned long long tot0, tot1 = 0ull;
+    const unsigned long long ex0 = block_excl_scan_u(pk0, tot0, sm);
+    unsigned long long ex1 = 0ull;
+    if (NCH > 5) ex1 = block_excl_scan_u(pk1, tot1, sm);
+    int run = 0;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+        const unsigned long long ex = i < 5 ? ex0 : ex1;
+        const unsigned long long tt = i < 5 ? tot0 : tot1;
+        const int sh = 12 * (i < 5 ? i : i - 5);
+        int pos = run + (int)((ex >> sh) & 0xfffull);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int q = i * E + e;
+            const float f = T.v[q];
+            if (finite_f(f) && f >= lo_v && f < hi_v) {
+                if (pos < kCapSlice) sm.stage[pos] = Cand{f, tile_index<ES>(geo, q)};
+                ++pos;
+            }
+        }
+        run += (int)((tt >> sh) & 0xfffull);
+    }
+    __syncthreads();
+    if (threadIdx.x < 64)
+        for (int p = threadIdx.x; p < min(run, kCapSlice); p += 64) pub_st_cand(&cands[p], sm.stage[p]);
+    return run;
+}
+
+// ---------------------------------------------------------------- streaming (slow path and rescans)
+
+// Streams slice s: fn(f, j) for every element.  Every thread runs the same number of iterations.
 template <int ES, class F>
 __device__ __forceinline__ void stream_slice(const DevGroup& G, const Ctx& c, int s, Smem& sm, F&& fn) {
     constexpr int E = 16 / ES;
     const Geo g = slice_geo<ES>(G, c, s);
-    if (c.counts) build_counts(G, c, g.lo, g.hi, sm);
+    if (c.counts) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
     const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+    const int nwords = (c.V + 31) >> 5;
     for (int ch = threadIdx.x; ch < g.nchunk; ch += kBlock) {
         const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
+        const MaskPair mk = mrow ? mask_pair(mrow, nwords, g.first + ch * E) : MaskPair{~0u, ~0u, 0};
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const int j = g.first + ch * E + e;
-            if (j >= g.lo && j < g.hi) fn(element(G, c, sm, mrow, g.lo, j, raw_elem<ES>(raw, e)), j);
+            if (j >= g.lo && j < g.hi) {
+                const int n = c.counts ? count_of(sm, j - g.first) : 0;
+                fn(transform(raw_elem<ES>(raw, e), j, n, mrow ? mask_bit(mk, j) : true, G, c, sm), j);
+            }
         }
     }
 }
 
 template <int ES, class F>
-__device__ __forceinline__ void visit(const DevGroup& G, const Ctx& c, Smem& sm, const Src& src, F&& fn) {
-    if (src.cand) {
-        for (int p = threadIdx.x; p < src.n; p += kBlock) fn(sm.u.cand.val[p], sm.u.cand.id[p]);
-    } else {
-        for (int s = 0; s < c.S; ++s) stream_slice<ES>(G, c, s, sm, fn);
-    }
+__device__ __forceinline__ void visit_row(const DevGroup& G, const Ctx& c, Smem& sm, F&& fn) {
+    for (int s = 0; s < c.S; ++s) stream_slice<ES>(G, c, s, sm, fn);
 }
 
 // Wave 0 scans 256 count bins from the top for the bin holding the rem-th largest element.
@@ -503,9 +1030,9 @@ __device__ __forceinline__ void pick_count_bin(int rem, Smem& sm) {
     }
 }
 
-// k-th largest finite value of the source; -inf when it holds fewer than k finite values.
+// k-th largest finite value of the row (streamed); -inf when it holds fewer than k finite values.
 template <int ES>
-__device__ __forceinline__ float select_kth(const DevGroup& G, const Ctx& c, Smem& sm, const Src& src, int k) {
+__device__ __forceinline__ float stream_kth(const DevGroup& G, const Ctx& c, Smem& sm, int k) {
     uint32_t prefix = 0u, pmask = 0u;
     int rem = k;
     for (int shift = 24; shift >= 0; shift -= 8) {
@@ -513,7 +1040,7 @@ __device__ __forceinline__ float select_kth(const DevGroup& G, const Ctx& c, Sme
         for (int b = threadIdx.x; b < 256; b += kBlock) sm.hcnt[b] = 0u;
         if (threadIdx.x == 0) sm.sel_bin = -1;
         __syncthreads();
-        visit<ES>(G, c, sm, src, [&](float f, int) {
+        visit_row<ES>(G, c, sm, [&](float f, int) {
             if (finite_f(f)) {
                 const uint32_t key = ord_key(f);
                 if ((key & pmask) == prefix) atomicAdd(&sm.hcnt[(key >> shift) & 255u], 1u);
@@ -523,7 +1050,7 @@ __device__ __forceinline__ float select_kth(const DevGroup& G, const Ctx& c, Sme
         pick_count_bin(rem, sm);
         __syncthreads();
         const int bin = sm.sel_bin;
-        if (bin < 0) return -INFINITY;  // fewer than k finite values (first round only)
+        if (bin < 0) return -INFINITY;
         rem = sm.sel_rem;
         prefix |= (uint32_t)bin << shift;
         pmask |= 255u << shift;
@@ -535,11 +1062,11 @@ __device__ __forceinline__ unsigned long long mass_q(float f, float m) {
     return (unsigned long long)((double)expf(f - m) * kMassScale);
 }
 
-// Smallest value v >= lower of the source with  sum{ q(x) : x > v, x >= lower } < target,  q = fixed-point
-// exp(x - m); +inf when no value qualifies (target <= 0).
+// Smallest value v >= lower of the row with sum{ q(x) : x > v, x >= lower } < target (q = fixed-point
+// exp(x - m)); +inf when none qualifies.
 template <int ES>
-__device__ __forceinline__ float select_mass(const DevGroup& G, const Ctx& c, Smem& sm, const Src& src, float lower,
-                                             float m, double target) {
+__device__ __forceinline__ float stream_mass(const DevGroup& G, const Ctx& c, Smem& sm, float lower, float m,
+                                             double target) {
     const uint32_t lkey = ord_key(lower);
     uint32_t prefix = 0u, pmask = 0u;
     unsigned long long acc = 0ull;
@@ -550,7 +1077,7 @@ __device__ __forceinline__ float select_mass(const DevGroup& G, const Ctx& c, Sm
             sm.hmass[b] = 0ull;
         }
         __syncthreads();
-        visit<ES>(G, c, sm, src, [&](float f, int) {
+        visit_row<ES>(G, c, sm, [&](float f, int) {
             if (finite_f(f)) {
                 const uint32_t key = ord_key(f);
                 if (key >= lkey && (key & pmask) == prefix) {
@@ -604,105 +1131,80 @@ __device__ __forceinline__ float select_mass(const DevGroup& G, const Ctx& c, Sm
     return key_float(prefix);
 }
 
-// The draw of engine/talker_sampler.py:168-172 over the survivors (finite values >= thr, minus the EOS id when
-// drop_eos): probabilities p = exp(x - m) * (1 / sum), their running sum in vocabulary order, the first survivor
-// whose running sum (rounded to float) exceeds u * total, or V - 1 when none does.
+// The draw of engine/talker_sampler.py:168-172 over survivors (finite values >= thr, minus the EOS id when
+// drop_eos), streaming the row: p = exp(x - m) * (1 / sum); the first survivor whose running sum, rounded to
+// float, exceeds u * total; V - 1 when none does.
 template <int ES>
-__device__ __forceinline__ int draw_token(const DevGroup& G, const Ctx& c, Smem& sm, const Src& src, float thr,
-                                          float m, bool drop_eos, float u) {
+__device__ __forceinline__ int stream_draw(const DevGroup& G, const Ctx& c, Smem& sm, float thr, float m,
+                                           bool drop_eos, float u) {
     auto survives = [&](float f, int j) { return finite_f(f) && f >= thr && !(drop_eos && j == G.eos); };
     double zpart = 0.0;
-    visit<ES>(G, c, sm, src, [&](float f, int j) {
+    visit_row<ES>(G, c, sm, [&](float f, int j) {
         if (survives(f, j)) zpart += (double)expf(f - m);
     });
-    const double zs = block_sum_d(zpart, sm);
-    const float inv = 1.0f / (float)zs;
-    const int ntiles = src.cand ? 1 : c.S;
+    const float inv = 1.0f / (float)block_sum_d(zpart, sm);
     double total = 0.0;
-    if (src.cand) {
+    for (int s = 0; s < c.S; ++s) {
         double part = 0.0;
-        visit<ES>(G, c, sm, src, [&](float f, int j) {
+        stream_slice<ES>(G, c, s, sm, [&](float f, int j) {
             if (survives(f, j)) part += (double)(expf(f - m) * inv);
         });
-        total = block_sum_d(part, sm);
-        if (threadIdx.x == 0) sm.tile_sum[0] = total;
-    } else {
-        for (int s = 0; s < c.S; ++s) {
-            double part = 0.0;
-            stream_slice<ES>(G, c, s, sm, [&](float f, int j) {
-                if (survives(f, j)) part += (double)(expf(f - m) * inv);
-            });
-            const double ts = block_sum_d(part, sm);
-            if (threadIdx.x == 0) sm.tile_sum[s] = ts;
-            total += ts;
-        }
+        const double ts = block_sum_d(part, sm);
+        if (threadIdx.x == 0) sm.tile_sum[s] = ts;
+        total += ts;
     }
     __syncthreads();
     const float target = u * (float)total;
     double base = 0.0;
-    for (int s = 0; s < ntiles; ++s) {
+    for (int s = 0; s < c.S; ++s) {
         const double ts = sm.tile_sum[s];
         if (!((float)(base + ts) > target)) {
             base += ts;
             continue;
         }
+        constexpr int E = 16 / ES;
+        const Geo g = slice_geo<ES>(G, c, s);
+        if (c.counts) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
+        const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+        const int nwords = (c.V + 31) >> 5;
         int found = INT_MAX;
-        if (src.cand) {
-            // vocabulary order = candidate order; rounds of kBlock consecutive candidates
-            double run_base = base;
-            for (int r0 = 0; r0 < src.n; r0 += kBlock) {
-                const int p = r0 + threadIdx.x;
-                const bool ok = p < src.n && survives(sm.u.cand.val[p], sm.u.cand.id[p]);
-                const double x = ok ? (double)(expf(sm.u.cand.val[p] - m) * inv) : 0.0;
-                double tot;
-                const double run = run_base + block_excl_scan_d(x, tot, sm) + x;
-                if (ok && (float)run > target) found = min(found, sm.u.cand.id[p]);
-                run_base += tot;
-                if (block_min_i(found, sm) != INT_MAX) break;
+        double run_base = base;
+        for (int r0 = 0; r0 < g.nchunk; r0 += kBlock) {
+            const int ch = r0 + threadIdx.x;
+            float pv[E];
+            int jv[E];
+            double mine = 0.0;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                pv[e] = 0.0f;
+                jv[e] = 0;
             }
-        } else {
-            constexpr int E = 16 / ES;
-            const Geo g = slice_geo<ES>(G, c, s);
-            if (c.counts) build_counts(G, c, g.lo, g.hi, sm);
-            const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
-            double run_base = base;
-            for (int r0 = 0; r0 < g.nchunk; r0 += kBlock) {
-                const int ch = r0 + threadIdx.x;
-                float pv[E];
-                int jv[E];
-                double mine = 0.0;
-                if (ch < g.nchunk) {
-                    const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        const int j = g.first + ch * E + e;
-                        jv[e] = j;
-                        pv[e] = 0.0f;
-                        if (j >= g.lo && j < g.hi) {
-                            const float f = element(G, c, sm, mrow, g.lo, j, raw_elem<ES>(raw, e));
-                            if (survives(f, j)) pv[e] = expf(f - m) * inv;
-                        }
-                        mine += (double)pv[e];
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < E; ++e) {
-                        pv[e] = 0.0f;
-                        jv[e] = 0;
-                    }
-                }
-                double tot;
-                double run = run_base + block_excl_scan_d(mine, tot, sm);
+            if (ch < g.nchunk) {
+                const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
+                const MaskPair mk = mrow ? mask_pair(mrow, nwords, g.first + ch * E) : MaskPair{~0u, ~0u, 0};
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
-                    if (pv[e] > 0.0f) {
-                        run += (double)pv[e];
-                        if ((float)run > target && found == INT_MAX) found = jv[e];
+                    const int j = g.first + ch * E + e;
+                    jv[e] = j;
+                    if (j >= g.lo && j < g.hi) {
+                        const int n = c.counts ? count_of(sm, j - g.first) : 0;
+                        const float f = transform(raw_elem<ES>(raw, e), j, n, mrow ? mask_bit(mk, j) : true, G, c, sm);
+                        if (survives(f, j)) pv[e] = expf(f - m) * inv;
                     }
+                    mine += (double)pv[e];
                 }
-                run_base += tot;
-                if (block_min_i(found, sm) != INT_MAX) break;
             }
+            double tot;
+            double run = run_base + block_excl_scan_d(mine, tot, sm);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if (pv[e] > 0.0f) {
+                    run += (double)pv[e];
+                    if ((float)run > target && found == INT_MAX) found = jv[e];
+                }
+            }
+            run_base += tot;
+            if (block_min_i(found, sm) != INT_MAX) break;
         }
         const int tok = block_min_i(found, sm);
         if (tok != INT_MAX) return tok;
@@ -776,16 +1278,14 @@ __device__ __forceinline__ void write_outputs(const DevGroup& G, const Ctx& c, S
         }
         return;
     }
-    const Src src{false, 0};
     auto keep = [&](float f, int j) { return f >= thr && !(drop_eos && j == G.eos); };
     double zpart = 0.0;
     if (qrow)
-        visit<ES>(G, c, sm, src, [&](float f, int j) {
+        visit_row<ES>(G, c, sm, [&](float f, int j) {
             if (finite_f(f) && keep(f, j)) zpart += (double)expf(f - m);
         });
-    const double zs = block_sum_d(zpart, sm);
-    const float inv = 1.0f / (float)zs;
-    visit<ES>(G, c, sm, src, [&](float f, int j) {
+    const float inv = 1.0f / (float)block_sum_d(zpart, sm);
+    visit_row<ES>(G, c, sm, [&](float f, int j) {
         const bool k = keep(f, j);
         if (prow) prow[j] = k ? f : -INFINITY;
         if (qrow) qrow[j] = !(m > -INFINITY) ? NAN : (k && finite_f(f)) ? expf(f - m) * inv : 0.0f;
@@ -839,214 +1339,729 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Ctx& c, in
     }
 }
 
+// The c-th largest (1 <= c <= 256) of the 256 per-thread values v: wave 0 sorts them descending with a bitonic
+// network (lane l holds positions 4l..4l+3; partners within a lane in registers, across lanes by shuffles).
+__device__ __forceinline__ float block_kth_of_256(float v, int c, Smem& sm) {
+    sm.tmax[threadIdx.x] = v;
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        float a[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) a[r] = sm.tmax[4 * lane + r];
+#pragma unroll
+        for (int k = 2; k <= 256; k <<= 1) {
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                if (j >= 4) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int i = 4 * lane + r;
+                        const float o = __shfl_xor(a[r], j >> 2);
+                        const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
+                        a[r] = keep_max ? fmaxf(a[r], o) : fminf(a[r], o);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (r & j) continue;
+                        const bool desc = ((4 * lane + r) & k) == 0;
+                        const float lo = a[r], hi = a[r | j];
+                        a[r] = desc ? fmaxf(lo, hi) : fminf(lo, hi);
+                        a[r | j] = desc ? fminf(lo, hi) : fmaxf(lo, hi);
+                    }
+                }
+            }
+        }
+        const int pos = c - 1, r = pos & 3;
+        const float x = r == 0 ? a[0] : r == 1 ? a[1] : r == 2 ? a[2] : a[3];
+        if (lane == (pos >> 2)) sm.sel_tau = x;
+    }
+    __syncthreads();
+    return sm.sel_tau;
+}
+
+// ---------------------------------------------------------------- cross-workgroup protocol
+
+// Every publication store of a slice is issued by wave 0 (threads 0..63).  Thread 0 waits until they have all
+// completed, then counts the slice in with a device-scope atomic; the slice that brings the count to S is the
+// row's last and finalises it (its publication loads are device-scope atomics too).  Returns true in the row's
+// last workgroup (every thread).
+__device__ __forceinline__ bool arrive_last(unsigned int* counter, int S, Smem& sm) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const unsigned int old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == (unsigned int)(S - 1);
+        if (last) pub_st(counter, 0u);  // every slice has arrived: reset for the next launch
+        sm.is_last = last;
+    }
+    __syncthreads();
+    return sm.is_last != 0;
+}
+
+// ---------------------------------------------------------------- finaliser pieces
+
+// Bitonic sort of sm.u.c.key[0, np) descending (np a power of two <= kCapRow).
+__device__ __forceinline__ void sort_keys_desc(Smem& sm, int np) {
+    for (int size = 2; size <= np; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int t = threadIdx.x; t < np / 2; t += kBlock) {
+                const int i = 2 * t - (t & (stride - 1));
+                const int j = i + stride;
+                const bool desc = (i & size) == 0;
+                const uint32_t a = sm.u.c.key[i], b = sm.u.c.key[j];
+                if ((a < b) == desc) {
+                    sm.u.c.key[i] = b;
+                    sm.u.c.key[j] = a;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// The top-k / top-p threshold from the sorted candidate keys (vocabulary counts n >= ...).  z_full is the
+// full-row normaliser (hf order); omni normalises over the top k (engine/talker_sampler.py:112,129).
+__device__ __forceinline__ float sorted_threshold(const Ctx& c, Smem& sm, int n, float m, double z_full) {
+    const int kk = min(c.k_eff, n);
+    const float thr_k = c.k_eff <= n ? key_float(sm.u.c.key[c.k_eff - 1]) : -INFINITY;
+    if (!c.p_active) return thr_k;
+    // blocked layout: thread t owns sorted positions [t*per, (t+1)*per)
+    const int per = (kk + kBlock - 1) / kBlock;
+    double mine = 0.0;
+    for (int r = threadIdx.x * per; r < min(kk, (int)(threadIdx.x + 1) * per); ++r)
+        mine += (double)expf(key_float(sm.u.c.key[r]) - m);
+    double ztop;
+    double run = block_excl_scan_d(mine, ztop, sm);
+    const double zp = c.hf ? z_full : ztop;
+    const double target = (double)c.top_p * zp;
+    int kp = 0;  // ranks whose exclusive mass is below top_p (a prefix)
+    for (int r = threadIdx.x * per; r < min(kk, (int)(threadIdx.x + 1) * per); ++r) {
+        if (run < target) ++kp;
+        run += (double)expf(key_float(sm.u.c.key[r]) - m);
+    }
+    kp = block_sum_i(kp, sm);
+    if (kp == kk && c.k_eff > n && zp < target) kp = c.k_eff;  // the top k's -inf ranks: exclusive mass = zp
+    const int kept = min(max(kp, c.min_keep_eff), c.k_eff);
+    return kept <= n ? key_float(sm.u.c.key[kept - 1]) : -INFINITY;
+}
+
+// Inverse-CDF draw over the LDS candidates (vocabulary order), survivors >= thr.
+__device__ __forceinline__ int cand_draw(const DevGroup& G, const Ctx& c, Smem& sm, int n, float thr, float m,
+                                         bool drop_eos, float u) {
+    const int per = (n + kBlock - 1) / kBlock;
+    const int lo = min(n, (int)threadIdx.x * per), hi = min(n, (int)(threadIdx.x + 1) * per);
+    auto surv = [&](int p) {
+        const float f = sm.u.c.val[p];
+        return f >= thr && !(drop_eos && sm.u.c.id[p] == G.eos);
+    };
+    double ze = 0.0;
+    for (int p = lo; p < hi; ++p)
+        if (surv(p)) ze += (double)expf(sm.u.c.val[p] - m);
+    const float inv = 1.0f / (float)block_sum_d(ze, sm);
+    double mine = 0.0;
+    for (int p = lo; p < hi; ++p)
+        if (surv(p)) mine += (double)(expf(sm.u.c.val[p] - m) * inv);
+    double total;
+    double run = block_excl_scan_d(mine, total, sm);
+    const float target = u * (float)total;
+    int found = INT_MAX;
+    for (int p = lo; p < hi; ++p)
+        if (surv(p)) {
+            run += (double)(expf(sm.u.c.val[p] - m) * inv);
+            if ((float)run > target) {
+                found = sm.u.c.id[p];
+                break;
+            }
+        }
+    const int tok = block_min_i(found, sm);
+    return tok == INT_MAX ? c.V - 1 : tok;
+}
+
+// Inverse-CDF draw from sub-block sums: sums[sbi] (already in units of exp(x - m), survivors only, flattened
+// slice-major in vocabulary order) locate the sub-block holding u * total; that sub-block is rescanned element
+// by element (survivors: finite values >= thr, minus EOS when drop_eos).
+template <int ES>
+__device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, Smem& sm, int nsb_total, float thr,
+                                              float m, bool drop_eos, float u) {
+    constexpr int E = 16 / ES;
+    constexpr int NSB = kNV / E * kWaves;
+    double zpart = 0.0;
+    for (int i = threadIdx.x; i < nsb_total; i += kBlock) zpart += sm.u.sbs[i];
+    const double zs = block_sum_d(zpart, sm);
+    const float inv = 1.0f / (float)zs;
+    const int per = (nsb_total + kBlock - 1) / kBlock;
+    const int lo = min(nsb_total, (int)threadIdx.x * per), hi = min(nsb_total, (int)(threadIdx.x + 1) * per);
+    double mine = 0.0;
+    for (int i = lo; i < hi; ++i) mine += sm.u.sbs[i] * (double)inv;
+    double total;
+    double run = block_excl_scan_d(mine, total, sm);
+    const float target = u * (float)total;
+    int first = INT_MAX;
+    for (int i = lo; i < hi; ++i) {
+        const double nxt = run + sm.u.sbs[i] * (double)inv;
+        if ((float)nxt > target) {
+            first = i;
+            break;
+        }
+        run = nxt;
+    }
+    first = block_min_i(first, sm);
+    // exclusive running sum before sub-block `first`
+    double before = (first != INT_MAX && first >= lo && first < hi) ? run : 0.0;
+    const int owner = first == INT_MAX ? -1 : first / max(per, 1);
+    __syncthreads();
+    if ((int)threadIdx.x == owner) sm.red_d[0] = before;
+    __syncthreads();
+    before = owner >= 0 ? sm.red_d[0] : 0.0;
+    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+    const int nwords = (c.V + 31) >> 5;
+    int cur_slice = -1;
+    for (int sbi = (first == INT_MAX ? nsb_total : first); sbi < nsb_total; ++sbi) {
+        const int s = sbi / NSB, sb = sbi % NSB;
+        const Geo g = slice_geo<ES>(G, c, s);
+        if (c.counts && s != cur_slice) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
+        cur_slice = s;
+        // 64 chunks: round sb / kWaves, wave sb % kWaves; wave 0 rescans them
+        int found = INT_MAX;
+        double sbsum = 0.0;
+        if (threadIdx.x < 64) {
+            const int ch = (sb / kWaves) * kBlock + (sb % kWaves) * 64 + (int)threadIdx.x;
+            float pv[E];
+            int jv[E];
+            double mine2 = 0.0;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                pv[e] = 0.0f;
+                jv[e] = 0;
+            }
+            if (ch < g.nchunk) {
+                const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
+                const MaskPair mk = mrow ? mask_pair(mrow, nwords, g.first + ch * E) : MaskPair{~0u, ~0u, 0};
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int j = g.first + ch * E + e;
+                    jv[e] = j;
+                    if (j >= g.lo && j < g.hi) {
+                        const int n = c.counts ? count_of(sm, j - g.first) : 0;
+                        const float f = transform(raw_elem<ES>(raw, e), j, n, mrow ? mask_bit(mk, j) : true, G, c, sm);
+                        if (finite_f(f) && f >= thr && !(drop_eos && j == G.eos)) pv[e] = expf(f - m) * inv;
+                    }
+                    mine2 += (double)pv[e];
+                }
+            }
+            // wave-level exclusive scan
+            double incl = mine2;
+            for (int o = 1; o < 64; o <<= 1) {
+                const double y = __shfl_up(incl, o);
+                if (lane_id() >= o) incl += y;
+            }
+            double r = before + incl - mine2;
+            (void)r;
+            double ex = __shfl_up(incl, 1);
+            if (lane_id() == 0) ex = 0.0;
+            double rr = before + ex;
+#pragma unroll
+            for (int e = 0; e < E; ++e)
+                if (pv[e] > 0.0f) {
+                    rr += (double)pv[e];
+                    if ((float)rr > target && found == INT_MAX) found = jv[e];
+                }
+            sbsum = __shfl(incl, 63);
+        }
+        const int tok = block_min_i(found, sm);
+        if (tok != INT_MAX) return tok;
+        if (threadIdx.x == 0) sm.red_d[1] = sbsum;
+        __syncthreads();
+        before += sm.red_d[1];
+    }
+    return c.V - 1;
+}
+
 // ---------------------------------------------------------------- finaliser
 
 template <int ES>
-__device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& sm, char* rws) {
-    if ((int)threadIdx.x < c.S) sm.summ[threadIdx.x] = ((const SliceSummary*)rws)[threadIdx.x];
+__device__ __forceinline__ void load_summaries(const Ctx& c, Smem& sm, const RowWs& w) {
+    if ((int)threadIdx.x < c.S) sm.summ[threadIdx.x] = pub_ld_summary(&w.summ[threadIdx.x]);
     __syncthreads();
+}
+
+// The slow, always-exact path: stream the row for every selection.
+template <int ES>
+__device__ __forceinline__ int slow_path(const DevGroup& G, const Ctx& c, Smem& sm, float m, double z, bool drop_eos,
+                                         float& thr) {
+    const float thr_k = stream_kth<ES>(G, c, sm, c.k_eff);
+    thr = thr_k;
+    if (c.p_active) {
+        double zp;
+        if (c.hf) {
+            zp = z;
+        } else {
+            double part = 0.0;
+            int ngt = 0;
+            visit_row<ES>(G, c, sm, [&](float f, int) {
+                if (finite_f(f) && f > thr_k) {
+                    part += (double)expf(f - m);
+                    ++ngt;
+                }
+            });
+            zp = block_sum_d(part, sm);
+            ngt = block_sum_i(ngt, sm);
+            if (thr_k > -INFINITY) zp += (double)(c.k_eff - ngt) * (double)expf(thr_k - m);
+        }
+        const float thr_p = stream_mass<ES>(G, c, sm, thr_k, m, (double)c.top_p * zp * kMassScale);
+        const float v_m = c.min_keep_eff <= 1 ? m : stream_kth<ES>(G, c, sm, c.min_keep_eff);
+        thr = fmaxf(fminf(thr_p, v_m), thr_k);
+    }
+    return stream_draw<ES>(G, c, sm, thr, m, drop_eos, row_uniform(G, c));
+}
+
+// Exact processed value of the EOS id (every thread must call: its history count is a block reduction).
+template <int ES>
+__device__ __forceinline__ float eos_value(const DevGroup& G, const Ctx& c, Smem& sm) {
+    int n = 0;
+    if (c.counts) {
+        const char* hrow = G.history + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
+        for (int i = threadIdx.x; i < G.hist_len; i += kBlock) {
+            const int64_t h = G.hist_i64 ? ((const int64_t*)hrow)[i] : (int64_t)((const int32_t*)hrow)[i];
+            n += h == (int64_t)G.eos;
+        }
+        n = block_sum_i(n, sm);
+    }
+    const char* rowp = G.logits + (int64_t)c.row * G.row_stride * ES;
+    float x;
+    if (ES == 2)
+        x = __uint_as_float((uint32_t)(*(const uint16_t*)(rowp + (int64_t)G.eos * 2)) << 16);
+    else
+        x = *(const float*)(rowp + (int64_t)G.eos * 4);
+    bool allowed = true;
+    if (G.allowed) allowed = ((G.allowed[(int64_t)c.row * G.allowed_stride + (G.eos >> 5)] >> (G.eos & 31)) & 1u) != 0;
+    return transform(x, G.eos, n, allowed, G, c, sm);
+}
+
+template <int ES>
+__device__ __forceinline__ void finish_row(const DevGroup& G, const Ctx& c, Smem& sm, int64_t tok, float thr, float m,
+                                           bool drop_eos) {
+    if (c.want_out) write_outputs<ES>(G, c, sm, c.greedy ? -INFINITY : thr, m, drop_eos);
+    update_state(G, c, tok);
+}
+
+template <int ES>
+__device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
+    constexpr int E = 16 / ES;
+    constexpr int NSB = kNV / E * kWaves;
+    load_summaries<ES>(c, sm, w);
     float m = -INFINITY, gmax = -INFINITY;
     double z = 0.0;
     int am = INT_MAX, ntot = 0;
     bool overflow = false;
     for (int s = 0; s < c.S; ++s) m = fmaxf(m, sm.summ[s].m);
     for (int s = 0; s < c.S; ++s) {
-        const SliceSummary q = sm.summ[s];
+        const SliceSummary& q = sm.summ[s];
         if (q.m == m && q.argmax < am) am = q.argmax;
         if (q.m > -INFINITY) z += q.z * exp((double)q.m - (double)m);
         gmax = fmaxf(gmax, q.g);
         ntot += q.ncand;
         overflow |= q.overflow != 0;
     }
+    Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
     const bool drop_eos = c.hf && c.censor;
-    int64_t tok;
+    const bool need_tok = G.tokens != nullptr || (G.flags & MIS_UPDATE_STATE);
+    int64_t tok = kPad;
     float thr = -INFINITY;
     if (c.greedy) {
         tok = am == INT_MAX ? c.V - 1 : am;
     } else if (!(m > -INFINITY)) {
         tok = c.V - 1;  // nothing allowed: the reference's clamp value
-    } else {
-        Src src{false, 0};
-        if (!c.full_draw) {
-            if (c.cand_mode && !overflow && ntot <= kCapRow) {
-                // candidates of all slices, in slice (= vocabulary) order
-                const Cand* cands = (const Cand*)(rws + sizeof(SliceSummary) * c.S);
-                int off = 0;
-                for (int s = 0; s < c.S; ++s) {
-                    const int n = sm.summ[s].ncand;
-                    for (int p = threadIdx.x; p < n; p += kBlock) {
-                        const Cand cd = cands[(int64_t)s * kCapSlice + p];
-                        sm.u.cand.val[off + p] = cd.f;
-                        sm.u.cand.id[off + p] = cd.j;
-                    }
-                    off += n;
+    } else if (c.full_draw) {
+        if (need_tok) {
+            // survivors = every finite value (minus a censored EOS): the published sub-block sums
+            const int nsb = c.S * NSB;
+            for (int i = threadIdx.x; i < nsb; i += kBlock) {
+                const int s = i / NSB;
+                const double sc = sm.summ[s].m > -INFINITY ? exp((double)sm.summ[s].m - (double)m) : 0.0;
+                sm.u.sbs[i] = pub_ld(&w.sb[(int64_t)s * kMaxSB + (i % NSB)]) * sc;
+            }
+            __syncthreads();
+            if (drop_eos) {
+                const float fe = eos_value<ES>(G, c, sm);
+                if (threadIdx.x == 0 && finite_f(fe)) {
+                    const int s = G.eos / c.slice_len;
+                    const Geo g = slice_geo<ES>(G, c, s);
+                    const int i = s * NSB + sub_block_of<ES>(g, G.eos);
+                    sm.u.sbs[i] = fmax(0.0, sm.u.sbs[i] - (double)expf(fe - m));
                 }
                 __syncthreads();
-                // every value >= gmax was published: the k-th largest is proven once k of them are >= gmax
-                int nge = 0;
-                for (int p = threadIdx.x; p < ntot; p += kBlock) nge += sm.u.cand.val[p] >= gmax ? 1 : 0;
-                nge = block_sum_i(nge, sm);
-                if (nge >= c.k_eff || gmax == -INFINITY) src = Src{true, ntot};
             }
-            const float thr_k = select_kth<ES>(G, c, sm, src, c.k_eff);
-            thr = thr_k;
-            if (c.p_active) {
-                double zp;
-                if (c.hf) {
-                    zp = z;  // full-vocabulary normaliser (engine/talker_sampler.py:112)
-                } else {
-                    // softmax over the top-k values (:129): those above thr_k plus (k - n_gt) copies of thr_k
-                    double part = 0.0;
-                    int ngt = 0;
-                    visit<ES>(G, c, sm, src, [&](float f, int) {
-                        if (finite_f(f) && f > thr_k) {
-                            part += (double)expf(f - m);
-                            ++ngt;
-                        }
-                    });
-                    zp = block_sum_d(part, sm);
-                    ngt = block_sum_i(ngt, sm);
-                    if (thr_k > -INFINITY) zp += (double)(c.k_eff - ngt) * (double)expf(thr_k - m);
-                }
-                const double target = (double)c.top_p * zp * kMassScale;
-                const float thr_p = select_mass<ES>(G, c, sm, src, thr_k, m, target);
-                const float v_m = c.min_keep_eff <= 1 ? m : select_kth<ES>(G, c, sm, src, c.min_keep_eff);
-                thr = fmaxf(fminf(thr_p, v_m), thr_k);
+            tok = sub_block_draw<ES>(G, c, sm, nsb, -INFINITY, m, drop_eos, row_uniform(G, c));
+        }
+    } else if (c.cand_mode && !overflow && ntot <= kCapRow) {
+        // candidates of all slices in vocabulary order, and their keys
+        int off = 0;
+        for (int s = 0; s < c.S; ++s) {
+            const int n = sm.summ[s].ncand;
+            for (int p = threadIdx.x; p < n; p += kBlock) {
+                const Cand cd = pub_ld_cand(&w.cand[(int64_t)s * kCapSlice + p]);
+                sm.u.c.val[off + p] = cd.f;
+                sm.u.c.id[off + p] = cd.j;
+                sm.u.c.key[off + p] = ord_key(cd.f);
+            }
+            off += n;
+        }
+        int np = 1;
+        while (np < ntot) np <<= 1;
+        for (int p = ntot + threadIdx.x; p < np; p += kBlock) sm.u.c.key[p] = 0u;
+        __syncthreads();
+        // every value >= gmax was published: the k-th largest is proven once k of them are >= gmax
+        int nge = 0;
+        for (int p = threadIdx.x; p < ntot; p += kBlock) nge += sm.u.c.val[p] >= gmax ? 1 : 0;
+        nge = block_sum_i(nge, sm);
+        if (nge >= c.k_eff || gmax == -INFINITY) {
+            sort_keys_desc(sm, np);
+            thr = sorted_threshold(c, sm, ntot, m, z);
+            if (need_tok) tok = cand_draw(G, c, sm, ntot, thr, m, drop_eos, row_uniform(G, c));
+        } else {
+            tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
+        }
+    } else if (c.nucleus) {
+        // merge the slices' mass histograms on the global 1/8-logit grid, below the row's top bin
+        const int HB = bin_of(m);
+        double gm = 0.0;
+        uint32_t gc = 0u;
+        const int o = threadIdx.x;  // one global bin per thread (kNB == kBlock)
+        for (int s = 0; s < c.S; ++s) {
+            const SliceSummary& q = sm.summ[s];
+            if (!(q.m > -INFINITY)) continue;
+            const int os = o - (HB - q.hb);
+            if (os >= 0 && os < kNB) {
+                gm += (double)pub_ld(&w.hmass[(int64_t)s * kNB + os]) * (1.0 / kMassScale) *
+                      exp((double)q.m - (double)m);
+                gc += pub_ld(&w.hcnt[(int64_t)s * kNB + os]);
             }
         }
-        const bool need_tok = G.tokens != nullptr || (G.flags & MIS_UPDATE_STATE);
-        tok = need_tok ? draw_token<ES>(G, c, sm, src, thr, m, drop_eos, row_uniform(G, c)) : kPad;
+        double ztot;
+        const double before = block_excl_scan_d(gm, ztot, sm);
+        const double target = (double)c.top_p * z;
+        const int bstar = block_max_i((gc > 0u && before < target) ? o : -1, sm);
+        int under = 0;
+        for (int s = 0; s < c.S; ++s) under += sm.summ[s].under_n;
+        const bool below_window = ztot < target && under > 0;  // the boundary may lie under the window
+        if (bstar >= 0 && bstar < kNB - 1 && !below_window) {
+            if (threadIdx.x == 0) {
+                Pending p;
+                p.mode = kPendNucleus;
+                p.lo_v = (float)(HB - bstar) / kBinScale;
+                p.hi_v = (float)(HB - bstar + 1) / kBinScale;
+                p.m = m;
+                p.z = z;
+                p.target = target;
+                *pend = p;
+                const unsigned int base = atomicAdd(&G.nhdr->n_items, (unsigned int)c.S);
+                for (int sl = 0; sl < c.S; ++sl) G.items[base + sl] = pack_item(G.gi, c.row, sl);
+            }
+            return;  // the nucleus pass draws and updates the state
+        }
+        tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
+    } else {
+        tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
     }
-    if (c.want_out) write_outputs<ES>(G, c, sm, thr, m, drop_eos);
-    update_state(G, c, tok);
+    if (threadIdx.x == 0) pend->mode = kPendNone;
+    finish_row<ES>(G, c, sm, tok, thr, m, drop_eos);
 }
 
-// ---------------------------------------------------------------- the row
+// ---------------------------------------------------------------- the slice phase
 
 template <int ES>
 __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
+    constexpr int E = 16 / ES;
+    constexpr int NCH = kNV / E;
     Ctx c;
     init_ctx(G, row, slice, c);
-    char* rws = G.ws + (int64_t)row * G.ws_row_bytes;
-    if (!c.live && !c.want_out) {
-        if (slice == 0 && threadIdx.x == 0 && G.tokens) G.tokens[row] = kPad;
-        return;
-    }
-    if (c.forced) {
+    const RowWs w = row_ws(G.ws + (int64_t)row * G.ws_row_bytes, c.S);
+    Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
+    if ((!c.live && !c.want_out) || c.forced) {
         if (slice != 0) return;
+        if (threadIdx.x == 0) pend->mode = kPendNone;
+        if (!c.forced) {
+            if (threadIdx.x == 0 && G.tokens) G.tokens[row] = kPad;
+            return;
+        }
         if (c.want_out) write_outputs<ES>(G, c, sm, -INFINITY, 0.0f, false);
         update_state(G, c, G.eos);
         return;
     }
     const Geo geo = slice_geo<ES>(G, c, slice);
-    if (c.counts) build_counts(G, c, geo.lo, geo.hi, sm);
     Tile T;
     load_tile<ES>(G, c, geo, T, sm);
     float tm = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < kNV; ++q)
-        if ((T.valid >> q) & 1ull) tm = fmaxf(tm, T.v[q]);
+    for (int q = 0; q < kNV; ++q) tm = fmaxf(tm, T.v[q]);
     const float m = block_max(tm, sm);
-    int first = INT_MAX;
+    int am = INT_MAX;
     if (c.greedy) {
+        // lowest slot holding m; out-of-slice slots hold -inf, so an all -inf slice answers its first element
+        int fq = kNV;
 #pragma unroll
-        for (int q = 0; q < kNV; ++q)
-            if (((T.valid >> q) & 1ull) && T.v[q] == m && first == INT_MAX) first = tile_index<ES>(geo, q);
+        for (int q = kNV - 1; q >= 0; --q) fq = T.v[q] == m ? q : fq;
+        const int first = fq < kNV ? tile_index<ES>(geo, fq) : INT_MAX;
+        am = m > -INFINITY ? block_min_i(first, sm) : geo.lo;
     }
-    const int am = block_min_i(first, sm);
     double z = 0.0;
-    if (!c.greedy && m > -INFINITY) {
-        double part = 0.0;
-#pragma unroll
-        for (int q = 0; q < kNV; ++q)
-            if ((T.valid >> q) & 1ull) part += (double)expf(T.v[q] - m);
-        z = block_sum_d(part, sm);
+    if (c.need_mass && m > -INFINITY) {
+        const double part = tile_sub_sums<ES>(T, m, -INFINITY, sm);
+        z = block_sum_d(part, sm);  // includes a barrier: sm.sbw is complete
+        if ((int)threadIdx.x < NCH * kWaves) pub_st(&w.sb[(int64_t)slice * kMaxSB + threadIdx.x], sm.sbw[threadIdx.x]);
     }
-    Cand* cands = (Cand*)(rws + sizeof(SliceSummary) * c.S) + (int64_t)slice * kCapSlice;
-    int ncand = 0, overflow = 0;
+    int ncand = 0, overflow = 0, hb = 0, under_n = 0;
+    unsigned long long under_q = 0ull;
     float g = INFINITY;
-    if (c.cand_mode) {
-        // tau = the cand_target-th largest per-thread maximum: at least cand_target values are >= tau
-        sm.tmax[threadIdx.x] = tm;
-        __syncthreads();
-        int rank = 0;
-        for (int u = 0; u < kBlock; ++u) {
-            const float o = sm.tmax[u];
-            rank += (o > tm) || (o == tm && u < (int)threadIdx.x);
+    if (c.nucleus && m > -INFINITY) {
+        hb = bin_of(m);
+        for (int b = threadIdx.x; b < kNB; b += kBlock) {
+            sm.hcnt[b] = 0u;
+            sm.hmass[b] = 0ull;
         }
-        if (rank == c.cand_target - 1) sm.sel_tau = tm;
         __syncthreads();
-        const float tau = sm.sel_tau;
-        g = tau;
-        // ordered compaction: round i, thread, element = vocabulary order
-        constexpr int E = 16 / ES;
-        constexpr int NCH = kNV / E;
-        int run = 0;
+        unsigned long long uq = 0ull;
+        int un = 0;
 #pragma unroll
-        for (int i = 0; i < NCH; ++i) {
-            int mine = 0;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const int q = i * E + e;
-                if (((T.valid >> q) & 1ull) && finite_f(T.v[q]) && T.v[q] >= tau) ++mine;
-            }
-            int tot;
-            int pos = run + block_excl_scan_i(mine, tot, sm);
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                const int q = i * E + e;
-                if (((T.valid >> q) & 1ull) && finite_f(T.v[q]) && T.v[q] >= tau) {
-                    if (pos < kCapSlice) cands[pos] = Cand{T.v[q], tile_index<ES>(geo, q)};
-                    ++pos;
+        for (int q = 0; q < kNV; ++q) {
+            const float f = T.v[q];
+            if (finite_f(f)) {
+                const int o = hb - bin_of(f);
+                const unsigned long long mq = mass_q(f, m);
+                if (o < kNB) {
+                    atomicAdd(&sm.hcnt[o], 1u);
+                    if (mq) atomicAdd(&sm.hmass[o], mq);
+                } else {
+                    uq += mq;
+                    ++un;
                 }
             }
-            run += tot;
         }
+        under_q = block_sum_u(uq, sm);
+        under_n = block_sum_i(un, sm);  // includes barriers: the histogram is complete
+        if (threadIdx.x < 64)
+            for (int b = threadIdx.x; b < kNB; b += 64) {
+                pub_st(&w.hcnt[(int64_t)slice * kNB + b], sm.hcnt[b]);
+                pub_st(&w.hmass[(int64_t)slice * kNB + b], sm.hmass[b]);
+            }
+    }
+    if (c.cand_mode) {
+        // tau = the cand_target-th largest per-thread maximum: at least cand_target values are >= tau
+        g = block_kth_of_256(tm, c.cand_target, sm);
+        const int run = publish_range<ES>(T, geo, g, INFINITY, w.cand + (int64_t)slice * kCapSlice, sm);
         ncand = min(run, kCapSlice);
         overflow = run > kCapSlice;
     }
+    (void)NCH;
     if (threadIdx.x == 0) {
-        SliceSummary* summ = (SliceSummary*)rws + slice;
-        summ->m = m;
-        summ->g = g;
-        summ->z = z;
-        summ->argmax = am;
-        summ->ncand = ncand;
-        summ->overflow = overflow;
+        SliceSummary s;
+        s.m = m;
+        s.g = g;
+        s.z = z;
+        s.argmax = am;
+        s.ncand = ncand;
+        s.overflow = overflow;
+        s.hb = hb;
+        s.under_q = under_q;
+        s.under_n = under_n;
+        s.n_hi = 0;
+        s.hi_mass = 0.0;
+        pub_st_summary(&w.summ[slice], s);
     }
     if (c.S > 1) {
-        __threadfence();  // release this slice's summary and candidates
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            unsigned int* counter = G.counters + G.row_begin + row;
-            const unsigned int old = atomicAdd(counter, 1u);
-            const int last = old == (unsigned int)(c.S - 1);
-            if (last) *counter = 0u;  // every slice has arrived: reset for the next launch
-            sm.is_last = last;
-        }
-        __syncthreads();
-        if (!sm.is_last) return;
-        __threadfence();  // acquire the other slices' writes
+        if (!arrive_last(G.counters + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
     } else {
         __syncthreads();
     }
-    finalize<ES>(G, c, sm, rws);
+    finalize<ES>(G, c, sm, w);
 }
 
-__global__ __launch_bounds__(kBlock) void sample_kernel(const KernelArgs args) {
-    __shared__ Smem sm;
+// ---------------------------------------------------------------- the nucleus pass
+
+template <int ES>
+__device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
+    constexpr int E = 16 / ES;
+    constexpr int NCH = kNV / E;
+    constexpr int NSB = NCH * kWaves;
+    Ctx c;
+    init_ctx(G, row, slice, c);
+    Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
+    const Pending P = *pend;
+    if (P.mode != kPendNucleus) return;
+    const RowWs w = row_ws(G.ws + (int64_t)row * G.ws_row_bytes, c.S);
+    const Geo geo = slice_geo<ES>(G, c, slice);
+    Tile T;
+    load_tile<ES>(G, c, geo, T, sm);
+    // everything above the boundary bin survives: its sums per sub-block; the bin's values go to the finaliser
+    const double part = tile_sub_sums<ES>(T, P.m, P.hi_v, sm);
+    int nhi = 0;
+#pragma unroll
+    for (int q = 0; q < kNV; ++q)
+        if (finite_f(T.v[q]) && T.v[q] >= P.hi_v) ++nhi;
+    const double hi_mass = block_sum_d(part, sm);
+    nhi = block_sum_i(nhi, sm);
+    if ((int)threadIdx.x < NSB) pub_st(&w.sb[(int64_t)slice * kMaxSB + threadIdx.x], sm.sbw[threadIdx.x]);
+    const int run = publish_range<ES>(T, geo, P.lo_v, P.hi_v, w.cand + (int64_t)slice * kCapSlice, sm);
+    if (threadIdx.x == 0) {
+        SliceSummary& s = w.summ[slice];
+        pub_st(&s.ncand, min(run, kCapSlice));
+        pub_st(&s.overflow, (int32_t)(run > kCapSlice));
+        pub_st(&s.n_hi, nhi);
+        pub_st(&s.hi_mass, hi_mass);
+    }
+    if (c.S > 1) {
+        if (!arrive_last(G.counters + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
+    } else {
+        __syncthreads();
+    }
+    // ---- finalise: exact top-p inside the boundary bin, then the draw
+    load_summaries<ES>(c, sm, w);
+    const float m = P.m;
+    const bool drop_eos = c.hf && c.censor;
+    int ntot = 0, nabove = 0;
+    bool overflow = false;
+    double above = 0.0;
+    for (int s = 0; s < c.S; ++s) {
+        ntot += sm.summ[s].ncand;
+        nabove += sm.summ[s].n_hi;
+        above += sm.summ[s].hi_mass;
+        overflow |= sm.summ[s].overflow != 0;
+    }
+    float thr = -INFINITY;
+    int64_t tok = kPad;
+    bool exact = !overflow && ntot <= kCapRow && ntot > 0 && above < P.target;
+    if (exact) {
+        int off = 0;
+        for (int s = 0; s < c.S; ++s) {
+            const int n = sm.summ[s].ncand;
+            for (int p = threadIdx.x; p < n; p += kBlock) {
+                const Cand cd = pub_ld_cand(&w.cand[(int64_t)s * kCapSlice + p]);
+                sm.u.c.val[off + p] = cd.f;
+                sm.u.c.id[off + p] = cd.j;
+                sm.u.c.key[off + p] = ord_key(cd.f);
+            }
+            off += n;
+        }
+        int np = 1;
+        while (np < ntot) np <<= 1;
+        for (int p = ntot + threadIdx.x; p < np; p += kBlock) sm.u.c.key[p] = 0u;
+        sort_keys_desc(sm, np);
+        // ranks inside the bin whose exclusive mass (above + bin values ranked before) is below the target
+        const int per = (ntot + kBlock - 1) / kBlock;
+        double mine = 0.0;
+        for (int r = threadIdx.x * per; r < min(ntot, (int)(threadIdx.x + 1) * per); ++r)
+            mine += (double)expf(key_float(sm.u.c.key[r]) - m);
+        double tot;
+        double run2 = above + block_excl_scan_d(mine, tot, sm);
+        int kp = 0;
+        for (int r = threadIdx.x * per; r < min(ntot, (int)(threadIdx.x + 1) * per); ++r) {
+            if (run2 < P.target) ++kp;
+            run2 += (double)expf(key_float(sm.u.c.key[r]) - m);
+        }
+        kp = block_sum_i(kp, sm);
+        const bool below_bin = kp == ntot && above + tot < P.target;  // the cut lies under the bin
+        int idx = below_bin ? -1 : kp - 1;  // position in the bin of the last kept rank
+        if (nabove + kp < c.min_keep_eff) idx = c.min_keep_eff - nabove - 1;  // min_keep clamp
+        exact = idx >= 0 && idx < ntot;
+        if (exact) thr = key_float(sm.u.c.key[idx]);
+    }
+    const bool need_tok = G.tokens != nullptr || (G.flags & MIS_UPDATE_STATE);
+    const float fe = drop_eos ? eos_value<ES>(G, c, sm) : -INFINITY;
+    if (!exact) {
+        tok = slow_path<ES>(G, c, sm, m, P.z, drop_eos, thr);
+    } else if (need_tok) {
+        // survivor sums per sub-block: the values above the bin (already summed) plus the bin's survivors.
+        // Candidates are in vocabulary order, so a sub-block's are a contiguous run (found by binary search).
+        const int nsb = c.S * NSB;
+        for (int i = threadIdx.x; i < nsb; i += kBlock) {
+            const int s = i / NSB, sb = i % NSB;
+            double v = pub_ld(&w.sb[(int64_t)s * kMaxSB + sb]);
+            const Geo g = slice_geo<ES>(G, c, s);
+            const int ch0 = (sb / kWaves) * kBlock + (sb % kWaves) * 64;
+            const int jlo = max(g.lo, g.first + ch0 * E), jhi = min(g.hi, g.first + (ch0 + 64) * E);
+            int a = 0, b = ntot;  // first candidate with id >= jlo
+            while (a < b) {
+                const int mid = (a + b) >> 1;
+                if (sm.u.c.id[mid] < jlo)
+                    a = mid + 1;
+                else
+                    b = mid;
+            }
+            for (int p = a; p < ntot && sm.u.c.id[p] < jhi; ++p) {
+                const float f = sm.u.c.val[p];
+                if (f >= thr && !(drop_eos && sm.u.c.id[p] == G.eos)) v += (double)expf(f - m);
+            }
+            if (drop_eos && G.eos >= jlo && G.eos < jhi && finite_f(fe) && fe >= P.hi_v)
+                v = fmax(0.0, v - (double)expf(fe - m));
+            pub_st(&w.sb[(int64_t)s * kMaxSB + sb], v);  // staged in global memory: LDS still holds the candidates
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < nsb; i += kBlock) sm.u.sbs[i] = pub_ld(&w.sb[(int64_t)(i / NSB) * kMaxSB + i % NSB]);
+        __syncthreads();
+        tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c));
+    }
+    if (threadIdx.x == 0) pend->mode = kPendNone;
+    finish_row<ES>(G, c, sm, tok, thr, m, drop_eos);
+}
+
+__device__ __forceinline__ bool locate(const KernelArgs& args, int& gi, int& row, int& slice) {
     const int bid = blockIdx.x;
     const int w = (bid % 8) * args.per_xcd + bid / 8;  // consecutive work items (a row's slices) share an XCD
-    if (w >= args.total_blocks) return;
-    int gi = 0;
+    if (w >= args.total_blocks) return false;
+    gi = 0;
     while (gi + 1 < args.n_groups && w >= args.g[gi + 1].block_begin) ++gi;
+    const int local = w - args.g[gi].block_begin;
+    row = local / args.g[gi].slices;
+    slice = local % args.g[gi].slices;
+    return true;
+}
+
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(const KernelArgs args) {
+    __shared__ Smem sm;
+    int gi, row, slice;
+    if (!locate(args, gi, row, slice)) return;
     const DevGroup& G = args.g[gi];
-    const int local = w - G.block_begin;
-    const int row = local / G.slices, slice = local % G.slices;
     if (G.es == 2)
         run_row<2>(G, row, slice, sm);
     else
         run_row<4>(G, row, slice, sm);
+}
+
+// Persistent pass over the work list the sample kernel's finalisers built (one item per slice of each pending
+// row).  Every workgroup leaves once the list is exhausted; the last one to leave clears the list.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args,
+                                                                                                   NucleusHeader* hdr,
+                                                                                                   const unsigned int* items) {
+    __shared__ Smem sm;
+    const unsigned int n = hdr->n_items;
+    if (n == 0u) return;  // nothing pending: the list is already clear
+    for (;;) {
+        if (threadIdx.x == 0) sm.item = atomicAdd(&hdr->next, 1u);
+        __syncthreads();
+        const unsigned int it = sm.item;
+        __syncthreads();
+        if (it >= n) break;
+        const unsigned int code = items[it];
+        const int gi = (int)(code >> 20), row = (int)((code >> 6) & 0x3fffu), slice = (int)(code & 63u);
+        const DevGroup& G = args.g[gi];
+        if (G.es == 2)
+            nucleus_row<2>(G, row, slice, sm);
+        else
+            nucleus_row<4>(G, row, slice, sm);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const unsigned int done = atomicAdd(&hdr->exited, 1u);
+        if (done == gridDim.x - 1) {
+            hdr->n_items = 0u;
+            hdr->next = 0u;
+            hdr->exited = 0u;
+        }
+    }
 }
 
 __global__ void uniform_kernel(const int64_t* seeds, const int64_t* steps, const int64_t* rids, int64_t n, int rng,
@@ -1074,10 +2089,17 @@ int fail(int code, const char* fmt, ...) {
 
 int max_slice_elems(int es) { return kBlock * kNV - 16 / es; }
 
-// Workspace: [arrival counters, kCounterBytes][per group: rows x (S summaries, S x kCapSlice candidates)].
-int64_t row_ws_bytes(int slices) {
-    const int64_t b = (int64_t)sizeof(SliceSummary) * slices + (int64_t)sizeof(Cand) * kCapSlice * slices;
-    return (b + 255) & ~(int64_t)255;
+// Workspace: [arrival counters, kCounterBytes][pending records, kPendingBytes][per group: rows x row regions].
+constexpr int64_t kFixedBytes = kCounterBytes + kPendingBytes + kHeaderBytes + kItemBytes;
+
+// Whether some row of the group can be a top-p-only row (no top-k), which needs the nucleus pass.
+bool may_need_nucleus(const MisGroup& g) {
+    const bool k_all = g.top_k != nullptr ||
+                       ((g.flags & MIS_TOPK_ZERO_DISABLES) && g.top_k_value <= 0) ||
+                       std::max(g.top_k_value, g.min_keep) >= g.vocab;
+    const bool p_on = g.top_p != nullptr || !((g.flags & MIS_TOPP_ONE_DISABLES) && g.top_p_value >= 1.0f);
+    const bool sampling = g.temperature != nullptr || g.temperature_value > 0.0f;
+    return k_all && p_on && sampling;
 }
 
 int check_group(const MisGroup& g, int idx) {
@@ -1124,7 +2146,7 @@ size_t mis_sizeof_group(void) { return sizeof(MisGroup); }
 
 size_t mis_workspace_bytes(const MisGroup* groups, int n_groups) {
     if (!groups || n_groups < 1 || n_groups > kMaxGroups) return 0;
-    size_t total = (size_t)kCounterBytes;
+    size_t total = (size_t)kFixedBytes;
     for (int i = 0; i < n_groups; ++i) {
         if (check_group(groups[i], i)) return 0;
         const int es = groups[i].dtype == MIS_BF16 ? 2 : 4;
@@ -1142,7 +2164,8 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     memset(&a, 0, sizeof a);
     a.n_groups = n_groups;
     int blocks = 0, rows_total = 0;
-    size_t ws_off = (size_t)kCounterBytes;
+    bool nucleus = false;
+    size_t ws_off = (size_t)kFixedBytes;
     for (int i = 0; i < n_groups; ++i) {
         const MisGroup& g = groups[i];
         if (int rc = check_group(g, i)) return rc;
@@ -1202,6 +2225,11 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
         d.ws_row_bytes = row_ws_bytes(d.slices);
         d.ws = (char*)workspace + ws_off;
         d.counters = (unsigned int*)workspace;
+        d.pending = (char*)workspace + kCounterBytes;
+        d.nhdr = (NucleusHeader*)((char*)workspace + kCounterBytes + kPendingBytes);
+        d.items = (unsigned int*)((char*)workspace + kCounterBytes + kPendingBytes + kHeaderBytes);
+        d.gi = i;
+        nucleus |= g.rows > 0 && may_need_nucleus(g);
         ws_off += (size_t)d.ws_row_bytes * (size_t)g.rows;
         const int64_t nb = (int64_t)g.rows * d.slices;
         if (nb + blocks > (int64_t)1 << 30) return fail(MIS_E_UNSUPPORTED, "too many rows");
@@ -1214,8 +2242,15 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     a.per_xcd = (blocks + 7) / 8;
     const int grid = a.per_xcd * 8;
     hipLaunchKernelGGL(sample_kernel, dim3(grid), dim3(kBlock), 0, (hipStream_t)stream, a);
-    const hipError_t e = hipGetLastError();
+    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
+    if (nucleus) {
+        hipLaunchKernelGGL(nucleus_kernel, dim3(kNucleusGrid), dim3(kBlock), 0, (hipStream_t)stream, a,
+                           (NucleusHeader*)((char*)workspace + kCounterBytes + kPendingBytes),
+                           (const unsigned int*)((char*)workspace + kCounterBytes + kPendingBytes + kHeaderBytes));
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
+    }
     return 0;
 }
 

@@ -123,7 +123,7 @@ def test_decode_streams_match_reference_golden(golden_streams, name, sem):
     frames, rows = int(c["frames"]), int(c["rows"])
     logits = torch.randn(frames, rows, V, generator=gen)
     logits[frames - 10, 1, EOS] = 1e4
-    assert float(logits.double().sum()) == float(c["logits_sum"])
+    assert abs(float(logits.double().sum()) - float(c["logits_sum"])) < 1e-9 * abs(float(c["logits_sum"]))
     st = hs.DecodeState.new([5 + i for i in range(rows)], cfg, device=DEV)
     toks = hs.decode_k(st, logits.to(DEV), EOS, cfg).cpu().numpy()
     assert np.array_equal(toks, c["tokens"])

@@ -185,7 +185,7 @@ def test_decode_streams_match_reference_golden(golden_streams, name, sem):
     frames, rows = int(c["frames"]), int(c["rows"])
     logits = torch.randn(frames, rows, V, generator=gen)
     logits[frames - 10, 1, EOS] = 1e4
-    assert float(logits.double().sum()) == float(c["logits_sum"])
+    assert abs(float(logits.double().sum()) - float(c["logits_sum"])) < 1e-9 * abs(float(c["logits_sum"]))
     st = ts.DecodeState.new([5 + i for i in range(rows)], cfg)
     assert np.array_equal(ts.decode_k(st, logits, EOS, cfg).numpy(), c["tokens"])
     assert np.array_equal(st.history.numpy(), c["history"]) and np.array_equal(st.steps.numpy(), c["steps"])
