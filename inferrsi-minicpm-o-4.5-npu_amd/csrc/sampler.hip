@@ -26,10 +26,10 @@
 //          holds the top-p boundary and leaves a pending record;
 //        anything the fast paths cannot prove exactly: streams the row again and
 //          selects by radix over order-preserving keys.
-// nucleus_kernel (a small persistent grid over a work list the finalisers built)
-// re-reads only the slices of pending rows, publishes the values inside the
-// boundary bin and the sums of everything above it, and its last workgroup per
-// row resolves the top-p threshold exactly and draws.
+// nucleus_kernel (the same grid; workgroups of rows without a pending record
+// leave at once) re-reads only the slices of pending rows, publishes the values
+// inside the boundary bin and the sums of everything above it, and its last
+// workgroup per row resolves the top-p threshold exactly and draws.
 // Workgroups never wait for one another: the only cross-workgroup protocol is
 // release / arrive / acquire on the per-row counter, which the finaliser resets
 // for the next launch.
@@ -66,28 +66,10 @@ constexpr int kMaxRows = 16384;      // rows per launch
 constexpr int kCounterStride = 32;  // u32 words between rows' counters: one 128-byte line each (no atomic contention)
 constexpr int64_t kCounterBytes = 4 * kCounterStride * (int64_t)kMaxRows;
 constexpr int64_t kPendingBytes = 64 * (int64_t)kMaxRows;
-constexpr int64_t kHeaderBytes = 512;                                  // nucleus work-list header
-constexpr int64_t kItemBytes = 4 * (int64_t)kMaxRows * kMaxSlices;     // nucleus work items
-constexpr int kNucleusGrid = 256;                                      // persistent workgroups of the nucleus pass
 constexpr int64_t kPad = -1;
 constexpr double kMassScale = 1099511627776.0;  // 2^40 fixed-point units of exp(x - max)
 
 enum : int32_t { kPendNone = 0, kPendNucleus = 1 };
-
-// Work list of the nucleus pass (each counter on its own 128-byte line); zero between launches.
-struct NucleusHeader {
-    unsigned int n_items;
-    unsigned int pad0[31];
-    unsigned int next;
-    unsigned int pad1[31];
-    unsigned int exited;
-    unsigned int pad2[31];
-};
-static_assert(sizeof(NucleusHeader) <= kHeaderBytes, "header");
-
-__host__ __device__ __forceinline__ unsigned int pack_item(int gi, int row, int slice) {
-    return ((unsigned)gi << 20) | ((unsigned)row << 6) | (unsigned)slice;
-}
 
 struct DevGroup {
     const char* logits;
@@ -136,8 +118,6 @@ struct DevGroup {
     char* ws;                // the group's row regions
     unsigned int* counters;  // arrival counters (fixed workspace prefix, zero between launches)
     char* pending;           // per-row pending records (fixed workspace region)
-    NucleusHeader* nhdr;     // nucleus work list header and items (fixed workspace region)
-    unsigned int* items;
     int32_t gi;              // index of this group in the launch
     int32_t pad2_;
     int64_t ws_row_bytes;
@@ -242,13 +222,13 @@ struct Smem {
     double tile_sum[kMaxSlices];
     SliceSummary summ[kMaxSlices];
     Cand stage[kCapSlice];  // a slice's published candidates, copied out by wave 0
+    int32_t coff[kMaxSlices + 1];  // finaliser: candidate offsets per slice
     int32_t sel_bin;
     int32_t sel_rem;
     int32_t is_last;
     int32_t pad_;
     unsigned long long sel_acc;
     float sel_tau;
-    unsigned int item;
 };
 
 __device__ __forceinline__ uint32_t ord_key(float f) {
@@ -492,6 +472,7 @@ __device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, 
     c.cand_target = min(per_slice, kBlock);
     c.cand_mode = filters && !c.full_draw && per_slice <= kBlock && c.k_eff <= kCapRow / 2;
     c.nucleus = filters && !c.full_draw && !c.cand_mode && c.k_eff >= c.V && c.p_active;
+    if (c.nucleus) c.cand_target = min(kBlock, kCapRow / (2 * c.S));  // a small nucleus resolves from these
     c.need_mass = c.full_draw || c.nucleus || (c.hf && filters && c.p_active);
 }
 
@@ -592,11 +573,21 @@ __device__ __forceinline__ int clear_counts(const DevGroup& G, const Ctx& c, int
     return bad;
 }
 
+__device__ __forceinline__ const char* hist_row(const DevGroup& G, int row) {
+    return G.history + (int64_t)row * G.hist_stride * (G.hist_i64 ? 8 : 4);
+}
+
+// int32 ids, 16-byte aligned rows, W % 4 == 0: the history is read as int4.
+__device__ __forceinline__ bool hist_vec(const DevGroup& G, const char* hrow) {
+    return !G.hist_i64 && (((uintptr_t)hrow) & 15) == 0 && (G.hist_len & 3) == 0;
+}
+
+// pre: the first kBlock * 4 int4 of the row's history, already loaded (vector layout only), or null.
 __device__ __forceinline__ int build_counts(const DevGroup& G, const Ctx& c, int base, int lo, int hi, int words,
-                                            Smem& sm) {
-    const char* hrow = G.history + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
+                                            Smem& sm, const int4* pre = nullptr) {
+    const char* hrow = hist_row(G, c.row);
     const int W = G.hist_len;
-    const bool vec = !G.hist_i64 && (((uintptr_t)hrow) & 15) == 0 && (W & 3) == 0;
+    const bool vec = hist_vec(G, hrow);
     int bad = 0;
     if (vec) {
         const int4* h4 = (const int4*)hrow;
@@ -606,7 +597,7 @@ __device__ __forceinline__ int build_counts(const DevGroup& G, const Ctx& c, int
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int i = b0 + u * kBlock + threadIdx.x;
-                v[u] = i < nv ? h4[i] : make_int4(-1, -1, -1, -1);
+                v[u] = (b0 == 0 && pre != nullptr) ? pre[u] : i < nv ? h4[i] : make_int4(-1, -1, -1, -1);
             }
             if (b0 == 0) {
                 bad = clear_counts(G, c, words, sm);
@@ -653,16 +644,21 @@ struct Geo {
 };
 
 template <int ES>
-__device__ __forceinline__ Geo slice_geo(const DevGroup& G, const Ctx& c, int s) {
+__device__ __forceinline__ Geo slice_geo_at(const DevGroup& G, int row, int s) {
     Geo g;
-    g.lo = s * c.slice_len;
-    g.hi = min(c.V, g.lo + c.slice_len);
-    const char* rowp = G.logits + (int64_t)c.row * G.row_stride * ES;
+    g.lo = s * G.slice_len;
+    g.hi = min(G.vocab, g.lo + G.slice_len);
+    const char* rowp = G.logits + (int64_t)row * G.row_stride * ES;
     const uintptr_t lo_addr = (uintptr_t)(rowp + (int64_t)g.lo * ES);
     g.base = lo_addr & ~(uintptr_t)15;
     g.first = g.lo - (int)((lo_addr - g.base) / ES);
     g.nchunk = (int)(((uintptr_t)(rowp + (int64_t)g.hi * ES) - g.base + 15) / 16);
     return g;
+}
+
+template <int ES>
+__device__ __forceinline__ Geo slice_geo(const DevGroup& G, const Ctx& c, int s) {
+    return slice_geo_at<ES>(G, c.row, s);
 }
 
 template <int ES>
@@ -720,23 +716,52 @@ __device__ __forceinline__ void issue_tile(const Geo& g, RawTile<ES>& R) {
 // any) allows it, and (omni order) it is not the censored EOS.  With the row's counts (sm.u.cnt, slot j - first)
 // and penalty table when its penalties apply.  Ends with a barrier; returns nonzero when the table holds an
 // alpha outside the corrected-reciprocal range.
-__device__ __forceinline__ int slice_prologue(const DevGroup& G, const Ctx& c, const Geo& g, int E, Smem& sm) {
-    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
-    const int wb = g.first >> 5;  // arithmetic shift: first may be negative in slice 0
-    const int eos = (!c.hf && c.censor) ? G.eos : -1;
+// The slice's other inputs, loaded right after its tile (before the row's parameters are known): the allowed
+// bits of the words covering it, limited to [lo, hi), and the first kBlock * 4 int4 of the row's history.
+struct Preload {
     uint32_t mw[2];
+    int4 h[4];
+    bool hvec;
+};
+
+__device__ __forceinline__ void preload(const DevGroup& G, int row, const Geo& g, Preload& P) {
+    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)row * G.allowed_stride : nullptr;
+    const int wb = g.first >> 5;  // arithmetic shift: first may be negative in slice 0
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int gw = wb + (int)threadIdx.x + u * kBlock;
         const int a = g.lo - 32 * gw, b = g.hi - 32 * gw;
         uint32_t m = (a <= 0 ? ~0u : a >= 32 ? 0u : ~0u << a) & (b >= 32 ? ~0u : b <= 0 ? 0u : (1u << b) - 1u);
         if (m != 0u && mrow != nullptr) m &= mrow[gw];  // m != 0: word gw meets [lo, hi), inside the row
-        if (eos >= 0 && (eos >> 5) == gw) m &= ~(1u << (eos & 31));
-        mw[u] = m;
+        P.mw[u] = m;
+    }
+    const char* hrow = G.history != nullptr && G.hist_len > 0 ? hist_row(G, row) : nullptr;
+    P.hvec = hrow != nullptr && hist_vec(G, hrow);
+    if (P.hvec) {
+        const int4* h4 = (const int4*)hrow;
+        const int nv = G.hist_len >> 2;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = u * kBlock + threadIdx.x;
+            P.h[u] = i < nv ? h4[i] : make_int4(-1, -1, -1, -1);
+        }
+    }
+}
+
+__device__ __forceinline__ int slice_prologue(const DevGroup& G, const Ctx& c, const Geo& g, int E, const Preload& P,
+                                              Smem& sm) {
+    const int wb = g.first >> 5;
+    const int eos = (!c.hf && c.censor) ? G.eos : -1;
+    uint32_t mw[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int gw = wb + (int)threadIdx.x + u * kBlock;
+        mw[u] = P.mw[u];
+        if (eos >= 0 && (eos >> 5) == gw) mw[u] &= ~(1u << (eos & 31));
     }
     int pen_bad = 0;
-    if (c.counts)
-        pen_bad = build_counts(G, c, g.first, g.lo, g.hi, g.nchunk * E / 2, sm);  // ends with a barrier
+    if (c.counts)  // ends with a barrier
+        pen_bad = build_counts(G, c, g.first, g.lo, g.hi, g.nchunk * E / 2, sm, P.hvec ? P.h : nullptr);
     else
         __syncthreads();  // the previous use of sm.mask is over
 #pragma unroll
@@ -861,12 +886,12 @@ __device__ __forceinline__ void process_tile_d(const DevGroup& G, const Ctx& c, 
         process_tile_t<ES, HF, COUNTS, kDivIeee>(G, c, g, R, T, sm);
 }
 
+// The prologue and the element pipeline over a tile whose loads are in flight.
 template <int ES>
-__device__ __forceinline__ void load_tile(const DevGroup& G, const Ctx& c, const Geo& g, Tile& T, Smem& sm) {
+__device__ __forceinline__ void finish_tile(const DevGroup& G, const Ctx& c, const Geo& g, const RawTile<ES>& R,
+                                            const Preload& P, Tile& T, Smem& sm) {
     constexpr int E = 16 / ES;
-    RawTile<ES> R;
-    issue_tile<ES>(g, R);
-    const int pen_bad = slice_prologue(G, c, g, E, sm);
+    const int pen_bad = slice_prologue(G, c, g, E, P, sm);
     // pow2: d = 2^k, so x * 2^-k is x / d correctly rounded for every x
     const bool pow2 = (__float_as_uint(c.tdiv) & 0x807fffffu) == 0u && c.tdiv >= 0x1p-126f && c.tdiv <= 0x1p126f;
     int mode = pow2 ? kDivPow2 : divisor_in_range(c.tdiv) ? kDivFast : kDivIeee;
@@ -1339,43 +1364,30 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Ctx& c, in
     }
 }
 
-// The c-th largest (1 <= c <= 256) of the 256 per-thread values v: wave 0 sorts them descending with a bitonic
-// network (lane l holds positions 4l..4l+3; partners within a lane in registers, across lanes by shuffles).
+// The c-th largest (1 <= c <= 256) of the 256 per-thread values v: a most-significant-bit-first radix select
+// over their order keys in wave 0 (4 keys per lane), counting each digit's keys with ballots.
 __device__ __forceinline__ float block_kth_of_256(float v, int c, Smem& sm) {
     sm.tmax[threadIdx.x] = v;
     __syncthreads();
     if (threadIdx.x < 64) {
         const int lane = threadIdx.x;
-        float a[4];
+        uint32_t k[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) a[r] = sm.tmax[4 * lane + r];
+        for (int r = 0; r < 4; ++r) k[r] = ord_key(sm.tmax[4 * lane + r]);
+        uint32_t prefix = 0u;
+        int need = c;
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t hm = ~0u << bit;
+            const uint32_t want = prefix | (1u << bit);
+            int cnt = 0;
 #pragma unroll
-        for (int k = 2; k <= 256; k <<= 1) {
-#pragma unroll
-            for (int j = k >> 1; j > 0; j >>= 1) {
-                if (j >= 4) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int i = 4 * lane + r;
-                        const float o = __shfl_xor(a[r], j >> 2);
-                        const bool keep_max = ((i & j) == 0) == ((i & k) == 0);
-                        a[r] = keep_max ? fmaxf(a[r], o) : fminf(a[r], o);
-                    }
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        if (r & j) continue;
-                        const bool desc = ((4 * lane + r) & k) == 0;
-                        const float lo = a[r], hi = a[r | j];
-                        a[r] = desc ? fmaxf(lo, hi) : fminf(lo, hi);
-                        a[r | j] = desc ? fminf(lo, hi) : fmaxf(lo, hi);
-                    }
-                }
-            }
+            for (int r = 0; r < 4; ++r) cnt += __popcll(__ballot((k[r] & hm) == want));
+            if (cnt >= need)
+                prefix = want;
+            else
+                need -= cnt;
         }
-        const int pos = c - 1, r = pos & 3;
-        const float x = r == 0 ? a[0] : r == 1 ? a[1] : r == 2 ? a[2] : a[3];
-        if (lane == (pos >> 2)) sm.sel_tau = x;
+        if (lane == 0) sm.sel_tau = key_float(prefix);
     }
     __syncthreads();
     return sm.sel_tau;
@@ -1402,31 +1414,91 @@ __device__ __forceinline__ bool arrive_last(unsigned int* counter, int S, Smem& 
 
 // ---------------------------------------------------------------- finaliser pieces
 
-// Bitonic sort of sm.u.c.key[0, np) descending (np a power of two <= kCapRow).
+// One bitonic compare-exchange step on 8 keys per lane (key index i = 8 * t + r): the lower index of each pair
+// keeps the larger key where the k-block sorts descending.
+template <int J>
+__device__ __forceinline__ void bitonic_lane_step(uint32_t (&a)[8], int t, int k) {
+    const bool desc_lane = ((8 * t) & k) == 0;  // the direction of every pair of the lane once k >= 8
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        if (r & J) continue;
+        const bool desc = k >= 8 ? desc_lane : ((8 * t + r) & k) == 0;
+        const uint32_t lo = min(a[r], a[r | J]), hi = max(a[r], a[r | J]);
+        a[r] = desc ? hi : lo;
+        a[r | J] = desc ? lo : hi;
+    }
+}
+
+// Sorts sm.u.c.key[0, np) descending (np a power of two in [8, kCapRow]; the keys past the candidates are zero,
+// below every real key).  Up to kBlock keys: rank sort.  Beyond: bitonic network over 8 keys per lane, partners
+// within a lane in registers, within a wave by shuffles, across waves through LDS (strides >= 512); up to 512 keys
+// are sorted by wave 0 alone.
 __device__ __forceinline__ void sort_keys_desc(Smem& sm, int np) {
-    for (int size = 2; size <= np; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            __syncthreads();
-            for (int t = threadIdx.x; t < np / 2; t += kBlock) {
-                const int i = 2 * t - (t & (stride - 1));
-                const int j = i + stride;
-                const bool desc = (i & size) == 0;
-                const uint32_t a = sm.u.c.key[i], b = sm.u.c.key[j];
-                if ((a < b) == desc) {
-                    sm.u.c.key[i] = b;
-                    sm.u.c.key[j] = a;
-                }
+    if (np <= kBlock) {
+        // rank sort: thread t counts the keys ahead of key t (larger, or equal at a lower position)
+        const int t = threadIdx.x;
+        const uint32_t mine = t < np ? sm.u.c.key[t] : 0u;
+        int rank = 0;
+        if (t < np) {
+#pragma unroll 2
+            for (int q = 0; q < np; q += 8) {  // np >= 8 is a power of two
+                const uint4 o0 = *(const uint4*)&sm.u.c.key[q];
+                const uint4 o1 = *(const uint4*)&sm.u.c.key[q + 4];
+                const uint32_t o[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) rank += (o[e] > mine || (o[e] == mine && q + e < t)) ? 1 : 0;
             }
         }
+        __syncthreads();
+        if (t < np) sm.u.c.key[rank] = mine;
+        __syncthreads();
+        return;
+    }
+    const int nw = np <= 512 ? 1 : kWaves;
+    const int N = 512 * nw;
+    if (wave_id() < nw) {
+        const int t = threadIdx.x;
+        uint32_t a[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) a[r] = 8 * t + r < np ? sm.u.c.key[8 * t + r] : 0u;
+        for (int k = 2; k <= N; k <<= 1) {
+            for (int j = k >> 1; j >= 8; j >>= 1) {
+                uint32_t b[8];
+                if (j >= 512) {
+                    __syncthreads();  // every wave is here: nw == kWaves
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) sm.u.c.key[8 * t + r] = a[r];
+                    __syncthreads();
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) b[r] = sm.u.c.key[(8 * t + r) ^ j];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) b[r] = __shfl_xor(a[r], j >> 3);
+                }
+                // j >= 8 and k > j: both bits come from the lane, not from r
+                const bool keep_max = (((8 * t) & j) == 0) == (((8 * t) & k) == 0);
+#pragma unroll
+                for (int r = 0; r < 8; ++r) a[r] = keep_max ? max(a[r], b[r]) : min(a[r], b[r]);
+            }
+            if (k >= 8) bitonic_lane_step<4>(a, t, k);
+            if (k >= 4) bitonic_lane_step<2>(a, t, k);
+            bitonic_lane_step<1>(a, t, k);
+        }
+        if (nw == kWaves) __syncthreads();  // the last cross-wave reads are done
+#pragma unroll
+        for (int r = 0; r < 8; ++r) sm.u.c.key[8 * t + r] = a[r];
     }
     __syncthreads();
 }
 
 // The top-k / top-p threshold from the sorted candidate keys (vocabulary counts n >= ...).  z_full is the
 // full-row normaliser (hf order); omni normalises over the top k (engine/talker_sampler.py:112,129).
-__device__ __forceinline__ float sorted_threshold(const Ctx& c, Smem& sm, int n, float m, double z_full) {
+// kept_out: the ranks kept; ztop_out: the mass of the first min(k, n) ranks (top-p rows only).
+__device__ __forceinline__ float sorted_threshold(const Ctx& c, Smem& sm, int n, float m, double z_full,
+                                                  int* kept_out = nullptr, double* ztop_out = nullptr) {
     const int kk = min(c.k_eff, n);
     const float thr_k = c.k_eff <= n ? key_float(sm.u.c.key[c.k_eff - 1]) : -INFINITY;
+    if (kept_out) *kept_out = min(c.k_eff, n);
     if (!c.p_active) return thr_k;
     // blocked layout: thread t owns sorted positions [t*per, (t+1)*per)
     const int per = (kk + kBlock - 1) / kBlock;
@@ -1435,7 +1507,7 @@ __device__ __forceinline__ float sorted_threshold(const Ctx& c, Smem& sm, int n,
         mine += (double)expf(key_float(sm.u.c.key[r]) - m);
     double ztop;
     double run = block_excl_scan_d(mine, ztop, sm);
-    const double zp = c.hf ? z_full : ztop;
+    const double zp = (c.hf || c.nucleus) ? z_full : ztop;  // a row without top-k normalises over the full row
     const double target = (double)c.top_p * zp;
     int kp = 0;  // ranks whose exclusive mass is below top_p (a prefix)
     for (int r = threadIdx.x * per; r < min(kk, (int)(threadIdx.x + 1) * per); ++r) {
@@ -1445,37 +1517,35 @@ __device__ __forceinline__ float sorted_threshold(const Ctx& c, Smem& sm, int n,
     kp = block_sum_i(kp, sm);
     if (kp == kk && c.k_eff > n && zp < target) kp = c.k_eff;  // the top k's -inf ranks: exclusive mass = zp
     const int kept = min(max(kp, c.min_keep_eff), c.k_eff);
+    if (kept_out) *kept_out = kept;
+    if (ztop_out) *ztop_out = ztop;
     return kept <= n ? key_float(sm.u.c.key[kept - 1]) : -INFINITY;
 }
 
-// Inverse-CDF draw over the LDS candidates (vocabulary order), survivors >= thr.
+// Inverse-CDF draw over the LDS candidates (vocabulary order), survivors >= thr: the first survivor whose
+// inclusive running mass exceeds u times the survivors' total (engine/talker_sampler.py:168-173 searchsorted).
 __device__ __forceinline__ int cand_draw(const DevGroup& G, const Ctx& c, Smem& sm, int n, float thr, float m,
                                          bool drop_eos, float u) {
     const int per = (n + kBlock - 1) / kBlock;
     const int lo = min(n, (int)threadIdx.x * per), hi = min(n, (int)(threadIdx.x + 1) * per);
-    auto surv = [&](int p) {
+    auto mass = [&](int p) {
         const float f = sm.u.c.val[p];
-        return f >= thr && !(drop_eos && sm.u.c.id[p] == G.eos);
+        return (f >= thr && !(drop_eos && sm.u.c.id[p] == G.eos)) ? (double)expf(f - m) : 0.0;
     };
-    double ze = 0.0;
-    for (int p = lo; p < hi; ++p)
-        if (surv(p)) ze += (double)expf(sm.u.c.val[p] - m);
-    const float inv = 1.0f / (float)block_sum_d(ze, sm);
     double mine = 0.0;
-    for (int p = lo; p < hi; ++p)
-        if (surv(p)) mine += (double)(expf(sm.u.c.val[p] - m) * inv);
+    for (int p = lo; p < hi; ++p) mine += mass(p);
     double total;
     double run = block_excl_scan_d(mine, total, sm);
-    const float target = u * (float)total;
+    const double target = (double)u * total;
     int found = INT_MAX;
-    for (int p = lo; p < hi; ++p)
-        if (surv(p)) {
-            run += (double)(expf(sm.u.c.val[p] - m) * inv);
-            if ((float)run > target) {
-                found = sm.u.c.id[p];
-                break;
-            }
+    for (int p = lo; p < hi; ++p) {
+        const double e = mass(p);
+        run += e;
+        if (e > 0.0 && run > target) {
+            found = sm.u.c.id[p];
+            break;
         }
+    }
     const int tok = block_min_i(found, sm);
     return tok == INT_MAX ? c.V - 1 : tok;
 }
@@ -1589,6 +1659,60 @@ __device__ __forceinline__ void load_summaries(const Ctx& c, Smem& sm, const Row
 }
 
 // The slow, always-exact path: stream the row for every selection.
+// The slices' published candidates into LDS in vocabulary order (slice s's at offset coff[s]) and the order keys
+// of those >= gate, packed in no particular order (nkeys of them) and padded with zeros up to np, the returned
+// power of two (>= 8).  ntot <= kCapRow.  The slice of each position comes from a map that every wave fills with
+// plain stores, so the loads that follow are all issued before any is used.
+__device__ __forceinline__ int gather_cands(const Ctx& c, Smem& sm, const RowWs& w, int ntot, float gate, int& nkeys) {
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const int x = l < c.S ? sm.summ[l].ncand : 0;
+        int incl = x;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o);
+            if (l >= o) incl += y;
+        }
+        sm.coff[l] = incl - x;
+        if (l == 63) sm.coff[kMaxSlices] = incl;
+        if (l == 0) sm.sel_rem = 0;  // key counter
+    }
+    __syncthreads();
+    uint8_t* smap = (uint8_t*)sm.hmass;  // kCapRow bytes, idle while a finaliser runs
+    for (int s = wave_id(); s < c.S; s += kWaves)
+        for (int p = sm.coff[s] + lane_id(); p < sm.coff[s + 1]; p += 64) smap[p] = (uint8_t)s;
+    __syncthreads();
+    constexpr int U = kCapRow / kBlock;
+    int sl[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = threadIdx.x + u * kBlock;
+        sl[u] = idx < ntot ? smap[idx] : 0;
+    }
+    Cand cd[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = threadIdx.x + u * kBlock;
+        cd[u] = Cand{-INFINITY, 0};
+        if (idx < ntot) cd[u] = pub_ld_cand(&w.cand[(int64_t)sl[u] * kCapSlice + (idx - sm.coff[sl[u]])]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int idx = threadIdx.x + u * kBlock;
+        if (idx < ntot) {
+            sm.u.c.val[idx] = cd[u].f;
+            sm.u.c.id[idx] = cd[u].j;
+            if (cd[u].f >= gate) sm.u.c.key[atomicAdd(&sm.sel_rem, 1)] = ord_key(cd[u].f);
+        }
+    }
+    __syncthreads();
+    nkeys = sm.sel_rem;
+    int np = 8;  // at least 8: the rank sort reads keys eight at a time
+    while (np < nkeys) np <<= 1;
+    for (int p = nkeys + threadIdx.x; p < np; p += kBlock) sm.u.c.key[p] = 0u;
+    __syncthreads();
+    return np;
+}
+
 template <int ES>
 __device__ __forceinline__ int slow_path(const DevGroup& G, const Ctx& c, Smem& sm, float m, double z, bool drop_eos,
                                          float& thr) {
@@ -1648,6 +1772,29 @@ __device__ __forceinline__ void finish_row(const DevGroup& G, const Ctx& c, Smem
     update_state(G, c, tok);
 }
 
+// A top-p row without top-k from the slices' candidates: sorted, the nucleus cut over the full normaliser z is
+// exact when it keeps only values >= gmax (every such value was published).  Returns false (LDS candidates
+// spent) when the candidates do not settle it.
+__device__ __forceinline__ bool nucleus_from_cands(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w, int ntot,
+                                                   bool overflow, float gmax, float m, double z, bool drop_eos,
+                                                   bool need_tok, float& thr, int64_t& tok) {
+    if (overflow || ntot <= 0 || ntot > kCapRow) return false;
+    int nge = 0;
+    const int np = gather_cands(c, sm, w, ntot, gmax, nge);
+    if (nge <= 0) return false;
+    sort_keys_desc(sm, np);
+    int kept = 0;
+    double zge = 0.0;
+    const float t = sorted_threshold(c, sm, nge, m, z, &kept, &zge);
+    // settled when the cut falls inside the values >= gmax: a kept rank past them, or their mass short of the
+    // target, would need values that were not published
+    const bool settled = gmax == -INFINITY || kept < nge || (kept == nge && zge >= (double)c.top_p * z);
+    if (!settled) return false;
+    thr = t;
+    if (need_tok) tok = cand_draw(G, c, sm, ntot, thr, m, drop_eos, row_uniform(G, c));
+    return true;
+}
+
 template <int ES>
 __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
     constexpr int E = 16 / ES;
@@ -1698,47 +1845,47 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
             tok = sub_block_draw<ES>(G, c, sm, nsb, -INFINITY, m, drop_eos, row_uniform(G, c));
         }
     } else if (c.cand_mode && !overflow && ntot <= kCapRow) {
-        // candidates of all slices in vocabulary order, and their keys
-        int off = 0;
-        for (int s = 0; s < c.S; ++s) {
-            const int n = sm.summ[s].ncand;
-            for (int p = threadIdx.x; p < n; p += kBlock) {
-                const Cand cd = pub_ld_cand(&w.cand[(int64_t)s * kCapSlice + p]);
-                sm.u.c.val[off + p] = cd.f;
-                sm.u.c.id[off + p] = cd.j;
-                sm.u.c.key[off + p] = ord_key(cd.f);
-            }
-            off += n;
-        }
-        int np = 1;
-        while (np < ntot) np <<= 1;
-        for (int p = ntot + threadIdx.x; p < np; p += kBlock) sm.u.c.key[p] = 0u;
-        __syncthreads();
-        // every value >= gmax was published: the k-th largest is proven once k of them are >= gmax
+        // candidates of all slices in vocabulary order; keys of those >= gmax
         int nge = 0;
-        for (int p = threadIdx.x; p < ntot; p += kBlock) nge += sm.u.c.val[p] >= gmax ? 1 : 0;
-        nge = block_sum_i(nge, sm);
+        const int np = gather_cands(c, sm, w, ntot, gmax, nge);
+        // every value >= gmax was published: the k-th largest is proven once k of them are >= gmax
         if (nge >= c.k_eff || gmax == -INFINITY) {
             sort_keys_desc(sm, np);
-            thr = sorted_threshold(c, sm, ntot, m, z);
+            thr = sorted_threshold(c, sm, nge, m, z);
             if (need_tok) tok = cand_draw(G, c, sm, ntot, thr, m, drop_eos, row_uniform(G, c));
         } else {
             tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
         }
+    } else if (c.nucleus && nucleus_from_cands(G, c, sm, w, ntot, overflow, gmax, m, z, drop_eos, need_tok, thr, tok)) {
+        // resolved from the published candidates
     } else if (c.nucleus) {
         // merge the slices' mass histograms on the global 1/8-logit grid, below the row's top bin
         const int HB = bin_of(m);
         double gm = 0.0;
         uint32_t gc = 0u;
         const int o = threadIdx.x;  // one global bin per thread (kNB == kBlock)
-        for (int s = 0; s < c.S; ++s) {
-            const SliceSummary& q = sm.summ[s];
-            if (!(q.m > -INFINITY)) continue;
-            const int os = o - (HB - q.hb);
-            if (os >= 0 && os < kNB) {
-                gm += (double)pub_ld(&w.hmass[(int64_t)s * kNB + os]) * (1.0 / kMassScale) *
-                      exp((double)q.m - (double)m);
-                gc += pub_ld(&w.hcnt[(int64_t)s * kNB + os]);
+        for (int s0 = 0; s0 < c.S; s0 += 8) {  // 8 slices' loads in flight at a time
+            unsigned long long hm[8];
+            uint32_t hc[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int s = s0 + u;
+                hm[u] = 0ull;
+                hc[u] = 0u;
+                if (s < c.S && sm.summ[s].m > -INFINITY) {
+                    const int os = o - (HB - sm.summ[s].hb);
+                    if (os >= 0 && os < kNB) {
+                        hm[u] = pub_ld(&w.hmass[(int64_t)s * kNB + os]);
+                        hc[u] = pub_ld(&w.hcnt[(int64_t)s * kNB + os]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int s = s0 + u;
+                if (hc[u] != 0u || hm[u] != 0ull)
+                    gm += (double)hm[u] * (1.0 / kMassScale) * exp((double)sm.summ[s].m - (double)m);
+                gc += hc[u];
             }
         }
         double ztot;
@@ -1758,8 +1905,6 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
                 p.z = z;
                 p.target = target;
                 *pend = p;
-                const unsigned int base = atomicAdd(&G.nhdr->n_items, (unsigned int)c.S);
-                for (int sl = 0; sl < c.S; ++sl) G.items[base + sl] = pack_item(G.gi, c.row, sl);
             }
             return;  // the nucleus pass draws and updates the state
         }
@@ -1777,6 +1922,13 @@ template <int ES>
 __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
     constexpr int E = 16 / ES;
     constexpr int NCH = kNV / E;
+    // the slice's loads go out before the row's parameters are read (those are scalar loads: they do not wait
+    // for the tile)
+    const Geo geo = slice_geo_at<ES>(G, row, slice);
+    RawTile<ES> R;
+    issue_tile<ES>(geo, R);
+    Preload P;
+    preload(G, row, geo, P);
     Ctx c;
     init_ctx(G, row, slice, c);
     const RowWs w = row_ws(G.ws + (int64_t)row * G.ws_row_bytes, c.S);
@@ -1792,9 +1944,8 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
         update_state(G, c, G.eos);
         return;
     }
-    const Geo geo = slice_geo<ES>(G, c, slice);
     Tile T;
-    load_tile<ES>(G, c, geo, T, sm);
+    finish_tile<ES>(G, c, geo, R, P, T, sm);
     float tm = -INFINITY;
 #pragma unroll
     for (int q = 0; q < kNV; ++q) tm = fmaxf(tm, T.v[q]);
@@ -1849,7 +2000,7 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
                 pub_st(&w.hmass[(int64_t)slice * kNB + b], sm.hmass[b]);
             }
     }
-    if (c.cand_mode) {
+    if (c.cand_mode || c.nucleus) {
         // tau = the cand_target-th largest per-thread maximum: at least cand_target values are >= tau
         g = block_kth_of_256(tm, c.cand_target, sm);
         const int run = publish_range<ES>(T, geo, g, INFINITY, w.cand + (int64_t)slice * kCapSlice, sm);
@@ -1887,15 +2038,19 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     constexpr int E = 16 / ES;
     constexpr int NCH = kNV / E;
     constexpr int NSB = NCH * kWaves;
-    Ctx c;
-    init_ctx(G, row, slice, c);
-    Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
+    Pending* pend = (Pending*)(G.pending + (int64_t)(G.row_begin + row) * sizeof(Pending));
     const Pending P = *pend;
     if (P.mode != kPendNucleus) return;
+    const Geo geo = slice_geo_at<ES>(G, row, slice);
+    RawTile<ES> R;
+    issue_tile<ES>(geo, R);
+    Preload PL;
+    preload(G, row, geo, PL);
+    Ctx c;
+    init_ctx(G, row, slice, c);
     const RowWs w = row_ws(G.ws + (int64_t)row * G.ws_row_bytes, c.S);
-    const Geo geo = slice_geo<ES>(G, c, slice);
     Tile T;
-    load_tile<ES>(G, c, geo, T, sm);
+    finish_tile<ES>(G, c, geo, R, PL, T, sm);
     // everything above the boundary bin survives: its sums per sub-block; the bin's values go to the finaliser
     const double part = tile_sub_sums<ES>(T, P.m, P.hi_v, sm);
     int nhi = 0;
@@ -1935,20 +2090,8 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     int64_t tok = kPad;
     bool exact = !overflow && ntot <= kCapRow && ntot > 0 && above < P.target;
     if (exact) {
-        int off = 0;
-        for (int s = 0; s < c.S; ++s) {
-            const int n = sm.summ[s].ncand;
-            for (int p = threadIdx.x; p < n; p += kBlock) {
-                const Cand cd = pub_ld_cand(&w.cand[(int64_t)s * kCapSlice + p]);
-                sm.u.c.val[off + p] = cd.f;
-                sm.u.c.id[off + p] = cd.j;
-                sm.u.c.key[off + p] = ord_key(cd.f);
-            }
-            off += n;
-        }
-        int np = 1;
-        while (np < ntot) np <<= 1;
-        for (int p = ntot + threadIdx.x; p < np; p += kBlock) sm.u.c.key[p] = 0u;
+        int nkeys = 0;
+        const int np = gather_cands(c, sm, w, ntot, -INFINITY, nkeys);
         sort_keys_desc(sm, np);
         // ranks inside the bin whose exclusive mass (above + bin values ranked before) is below the target
         const int per = (ntot + kBlock - 1) / kBlock;
@@ -2031,37 +2174,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         run_row<4>(G, row, slice, sm);
 }
 
-// Persistent pass over the work list the sample kernel's finalisers built (one item per slice of each pending
-// row).  Every workgroup leaves once the list is exhausted; the last one to leave clears the list.
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args,
-                                                                                                   NucleusHeader* hdr,
-                                                                                                   const unsigned int* items) {
+// The nucleus pass over the sample kernel's grid: the workgroups of rows with a pending record redo their slice
+// and resolve the row; every other workgroup leaves after reading that record.
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args) {
     __shared__ Smem sm;
-    const unsigned int n = hdr->n_items;
-    if (n == 0u) return;  // nothing pending: the list is already clear
-    for (;;) {
-        if (threadIdx.x == 0) sm.item = atomicAdd(&hdr->next, 1u);
-        __syncthreads();
-        const unsigned int it = sm.item;
-        __syncthreads();
-        if (it >= n) break;
-        const unsigned int code = items[it];
-        const int gi = (int)(code >> 20), row = (int)((code >> 6) & 0x3fffu), slice = (int)(code & 63u);
-        const DevGroup& G = args.g[gi];
-        if (G.es == 2)
-            nucleus_row<2>(G, row, slice, sm);
-        else
-            nucleus_row<4>(G, row, slice, sm);
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) {
-        const unsigned int done = atomicAdd(&hdr->exited, 1u);
-        if (done == gridDim.x - 1) {
-            hdr->n_items = 0u;
-            hdr->next = 0u;
-            hdr->exited = 0u;
-        }
-    }
+    int gi, row, slice;
+    if (!locate(args, gi, row, slice)) return;
+    const DevGroup& G = args.g[gi];
+    if (G.es == 2)
+        nucleus_row<2>(G, row, slice, sm);
+    else
+        nucleus_row<4>(G, row, slice, sm);
 }
 
 __global__ void uniform_kernel(const int64_t* seeds, const int64_t* steps, const int64_t* rids, int64_t n, int rng,
@@ -2090,7 +2213,7 @@ int fail(int code, const char* fmt, ...) {
 int max_slice_elems(int es) { return kBlock * kNV - 16 / es; }
 
 // Workspace: [arrival counters, kCounterBytes][pending records, kPendingBytes][per group: rows x row regions].
-constexpr int64_t kFixedBytes = kCounterBytes + kPendingBytes + kHeaderBytes + kItemBytes;
+constexpr int64_t kFixedBytes = kCounterBytes + kPendingBytes;
 
 // Whether some row of the group can be a top-p-only row (no top-k), which needs the nucleus pass.
 bool may_need_nucleus(const MisGroup& g) {
@@ -2226,8 +2349,6 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
         d.ws = (char*)workspace + ws_off;
         d.counters = (unsigned int*)workspace;
         d.pending = (char*)workspace + kCounterBytes;
-        d.nhdr = (NucleusHeader*)((char*)workspace + kCounterBytes + kPendingBytes);
-        d.items = (unsigned int*)((char*)workspace + kCounterBytes + kPendingBytes + kHeaderBytes);
         d.gi = i;
         nucleus |= g.rows > 0 && may_need_nucleus(g);
         ws_off += (size_t)d.ws_row_bytes * (size_t)g.rows;
@@ -2245,9 +2366,7 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
     if (nucleus) {
-        hipLaunchKernelGGL(nucleus_kernel, dim3(kNucleusGrid), dim3(kBlock), 0, (hipStream_t)stream, a,
-                           (NucleusHeader*)((char*)workspace + kCounterBytes + kPendingBytes),
-                           (const unsigned int*)((char*)workspace + kCounterBytes + kPendingBytes + kHeaderBytes));
+        hipLaunchKernelGGL(nucleus_kernel, dim3(grid), dim3(kBlock), 0, (hipStream_t)stream, a);
         e = hipGetLastError();
         if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
     }
