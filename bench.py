@@ -1,6 +1,7 @@
 """Sampled rows/s and HBM-roofline fraction of the fused sampling kernel on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload thinker_b64] [--no-cpu-baseline]
+    python bench.py --copy-calibration      # a plain 512 MiB device copy, for scaling rocprof's byte counters
 
 A step is one launch of the fused pipeline + draw over one batch of synthetic
 logits resident in HBM (default: the Thinker batch-64 step — vocab 151,748
@@ -9,6 +10,14 @@ bf16, heterogeneous top-k / top-p / temperature, repetition 1.1 over
 enough copies of the logits that no copy is still cached (the 256 MB
 last-level cache) when it is read again, and are replayed from a HIP graph so
 the host never throttles the queue.  Prints one JSON line on stdout.
+
+A step is the sample kernel plus, when a row of the batch has top-p without
+top-k and a nucleus too large for the first pass, the nucleus kernel; the
+roofline figure divides the step's algorithmic bytes by the step time.  Its
+``traffic`` (HBM bytes per step) comes from the rocprof FETCH_SIZE and
+WRITE_SIZE counters recorded in profiles/traffic_thinker_b64.json, each scaled
+by what the counter reads for the copy of --copy-calibration; it is null when
+that file is absent.
 """
 
 from __future__ import annotations
@@ -28,6 +37,8 @@ for _p in (str(ROOT), str(ROOT / "inferrsi-minicpm-o-4.5-npu_amd")):
 METRIC = "sampled rows/sec + % HBM roofline, vocab 151,748 bf16, batch 64"
 HBM_PEAK_GBS = 8000.0
 LLC_BYTES = 256 << 20
+COPY_BYTES = 512 << 20
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_thinker_b64.json"
 
 
 def log(*a) -> None:
@@ -56,6 +67,31 @@ def cpu_baseline(wl, budget_s: float) -> dict:
                       f"pipeline (processed logits, draw) in {el:.1f} s"}
 
 
+def copy_calibration() -> int:
+    """A device-to-device copy of COPY_BYTES, ten times: reads and writes COPY_BYTES per launch."""
+    import torch
+
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda:0").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {COPY_BYTES} bytes 10 times")
+    return 0
+
+
+def traffic_per_step(workload: str):
+    """HBM bytes per step from the recorded counters (None when there is no record for this workload)."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    rec = json.loads(TRAFFIC_FILE.read_text())
+    if rec.get("workload") != workload:
+        return None
+    fetch = sum(rec["fetch_kib_per_step"].values()) * 1024 * rec["fetch_scale"]
+    write = sum(rec["write_kib_per_step"].values()) * 1024 * rec["write_scale"]
+    return fetch + write
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -64,7 +100,10 @@ def main() -> int:
     ap.add_argument("--workload", default="thinker_b64")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", action="store_true")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         log(f"bench.py measures one GPU: the sampling path runs on a single MI355X (asked for --gpus {args.gpus}); "
             "rows shard across GPUs without any exchange, so N GPUs would simply run N independent copies")
@@ -133,7 +172,7 @@ def main() -> int:
                    "rows": wl.rows, "vocab": wl.vocab, "bytes_per_step": nbytes, "rotating_copies": rotate,
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic_per_step(wl.name)},
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(wl_cpu, args.cpu_budget)

@@ -45,6 +45,8 @@ enum {
     MIS_TOPK_ZERO_DISABLES = 1, /* top_k <= 0 means "no top-k" (vLLM); otherwise k = min(max(top_k, min_keep), V) */
     MIS_TOPP_ONE_DISABLES = 2,  /* top_p >= 1 means "no top-p"; otherwise the reference formula is evaluated at p = 1 */
     MIS_UPDATE_STATE = 4,       /* live rows: append the token to history, steps += 1, finished |= (token == eos) */
+    MIS_FINALIZE_STREAMING = 8, /* finalise every row from its logits alone (the path a row takes when its slice
+                                   workgroups did not share an XCD); same results, slower; for validation */
 };
 
 enum { MIS_E_ARG = 1, MIS_E_WORKSPACE = 2, MIS_E_UNSUPPORTED = 3 };
@@ -59,7 +61,7 @@ typedef struct MisGroup {
     int32_t vocab;                 /* V >= 1 */
     int32_t rows;                  /* B >= 0 */
     int32_t semantics;             /* MIS_OMNI | MIS_HF */
-    int32_t flags;                 /* MIS_TOPK_ZERO_DISABLES | MIS_TOPP_ONE_DISABLES | MIS_UPDATE_STATE */
+    int32_t flags;                 /* MIS_TOPK_ZERO_DISABLES | MIS_TOPP_ONE_DISABLES | MIS_UPDATE_STATE | ... */
     int32_t min_keep;              /* >= 1 (reference: 3 for hf, 1 for omni) */
 
     const float* temperature;      /* [rows] or NULL; T <= 0 selects greedy (first index of the max) */

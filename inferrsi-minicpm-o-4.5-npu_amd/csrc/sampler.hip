@@ -1,38 +1,42 @@
 // Fused token-sampling kernels for MI355X (gfx950) behind the C-ABI of include/mi355x_sampler.h.
 //
 // A row of V logits is cut into S vocabulary slices of at most ~10K elements,
-// one 256-thread workgroup each (XCD-aware: a row's slices share an XCD).
+// one 256-thread workgroup each.  Whole rows are assigned to XCDs, so a row's
+// slices share an L2.
 //
 // sample_kernel, per slice workgroup:
-//   1. counts the row's history ids that fall in the slice into an LDS table,
-//   2. reads the slice once (16-byte vector loads of logits and mask words) and
+//   1. issues the slice's 16-byte logit loads, its allowed-mask words and the
+//      row's history, then reads the row's parameters,
+//   2. counts the history ids that fall in the slice into an LDS table and
 //      applies the row's pipeline element by element — EOS censor, repetition /
 //      frequency / presence penalties, allowed-token bitmask, temperature, in
 //      the order of engine/talker_sampler.py:142-156 — keeping the values in
 //      registers,
 //   3. publishes a summary (max, first argmax, sum of exp relative to its max,
-//      per-sub-block sums) and, by row kind, its top-k candidates (every value
-//      >= tau, the c-th largest per-thread maximum, in vocabulary order) or a
-//      probability-mass histogram on a fixed grid of 1/8 logit,
-//   4. increments the row's arrival counter.  The last workgroup to arrive
+//      per-sub-block sums) and, by row kind, its candidates (every value >= tau,
+//      the c-th largest per-thread maximum, in vocabulary order) and for top-p
+//      rows without top-k also a probability-mass histogram on a 1/8-logit grid,
+//   4. counts itself in on the row's arrival word.  The last workgroup to arrive
 //      finalises the row:
 //        greedy rows: first index of the maximum;
-//        top-k rows: sorts the candidate values (bitonic, LDS), reads the
-//          top-k threshold, the top-p cut over the sorted masses and draws by
-//          inverse CDF over the candidates in vocabulary order;
+//        top-k rows and small nuclei: sorts the candidate keys (rank sort or a
+//          register bitonic network), reads the top-k threshold and the top-p
+//          cut over the sorted masses, and draws by inverse CDF over the
+//          candidates in vocabulary order;
 //        unfiltered rows: walks the sub-block sums to the sub-block holding
 //          u * total and rescans only that sub-block;
-//        top-p-only rows (no top-k): merges the histograms, finds the bin that
-//          holds the top-p boundary and leaves a pending record;
-//        anything the fast paths cannot prove exactly: streams the row again and
-//          selects by radix over order-preserving keys.
+//        larger nuclei: merges the histograms, finds the bin that holds the
+//          top-p boundary and leaves a pending record;
+//        anything the fast paths cannot prove exactly, or a row whose slices
+//          ran on more than one XCD: streams the row again and selects by radix
+//          over order-preserving keys.
 // nucleus_kernel (the same grid; workgroups of rows without a pending record
 // leave at once) re-reads only the slices of pending rows, publishes the values
 // inside the boundary bin and the sums of everything above it, and its last
 // workgroup per row resolves the top-p threshold exactly and draws.
 // Workgroups never wait for one another: the only cross-workgroup protocol is
-// release / arrive / acquire on the per-row counter, which the finaliser resets
-// for the next launch.
+// publish / arrive / read on the per-row arrival word, which the finaliser
+// resets for the next launch.
 
 #include <hip/hip_runtime.h>
 
@@ -123,12 +127,14 @@ struct DevGroup {
     int64_t ws_row_bytes;
 };
 
+// Whole rows are assigned to XCDs: block b runs on XCD b % 8 (the dispatcher's round-robin), as the (b / 8)-th
+// slice of that XCD's rows, which are rows [seg_row[x][g], + seg_rows[x][g]) of each group g in turn.
 struct KernelArgs {
     DevGroup g[kMaxGroups];
     int32_t n_groups;
-    int32_t total_blocks;
     int32_t per_xcd;
-    int32_t pad_;
+    int32_t seg_row[8][kMaxGroups];
+    int32_t seg_rows[8][kMaxGroups];
 };
 
 struct SliceSummary {
@@ -226,6 +232,7 @@ struct Smem {
     int32_t sel_bin;
     int32_t sel_rem;
     int32_t is_last;
+    int32_t foreign;  // the row's slices ran on more than one XCD: their publications are not readable here
     int32_t pad_;
     unsigned long long sel_acc;
     float sel_tau;
@@ -247,13 +254,16 @@ __device__ __forceinline__ int bin_of(float f) {
 }
 
 // ---------------------------------------------------------------- cross-workgroup publication
-// Data one workgroup publishes for another (summaries, sums, histograms, candidates) is written and read with
-// relaxed device-scope atomic stores and loads, which are coherent across XCDs without writing back or
-// invalidating whole caches; the publisher orders them before its arrival count by waiting for its stores.
+// Data one workgroup publishes for another (summaries, sums, histograms, candidates) goes out as plain stores,
+// which the CU's write-through L1 passes to the L2, and is read back with relaxed device-scope atomic loads, which
+// bypass the reader's L1 and read the L2.  The publisher orders its stores before its arrival count by waiting
+// for them.  Every workgroup of a row runs on one XCD (the block-to-row mapping groups a row's slices by
+// blockIdx % 8, the stride of the dispatcher's round-robin over XCDs), so they share that L2: no cache writeback
+// or invalidation is needed, and nothing is written through to HBM.
 
 template <class T>
 __device__ __forceinline__ void pub_st(T* p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *p = v;
 }
 
 template <class T>
@@ -1395,18 +1405,32 @@ __device__ __forceinline__ float block_kth_of_256(float v, int c, Smem& sm) {
 
 // ---------------------------------------------------------------- cross-workgroup protocol
 
+__device__ __forceinline__ unsigned xcc_id() {
+    unsigned x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 7u;
+}
+
 // Every publication store of a slice is issued by wave 0 (threads 0..63).  Thread 0 waits until they have all
-// completed, then counts the slice in with a device-scope atomic; the slice that brings the count to S is the
-// row's last and finalises it (its publication loads are device-scope atomics too).  Returns true in the row's
-// last workgroup (every thread).
+// completed, then counts the slice in with a device-scope atomic on the row's 64-bit arrival word, which holds
+// one 7-bit count per XCD.  The slice that completes the count (S arrivals) is the row's last and finalises it.
+// It also learns whether every slice ran on its own XCD: if one did not, the slices' publications may sit in
+// another XCD's L2, and the finaliser must not read them (sm.foreign).  Returns true in the row's last workgroup
+// (every thread).
 __device__ __forceinline__ bool arrive_last(unsigned int* counter, int S, Smem& sm) {
     __syncthreads();
     if (threadIdx.x == 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const unsigned int old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int last = old == (unsigned int)(S - 1);
-        if (last) pub_st(counter, 0u);  // every slice has arrived: reset for the next launch
+        unsigned long long* word = (unsigned long long*)counter;
+        const unsigned x = xcc_id();
+        const unsigned long long old =
+            __hip_atomic_fetch_add(word, 1ull << (7 * x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int total = 1;
+        for (int f = 0; f < 8; ++f) total += (int)((old >> (7 * f)) & 127ull);
+        const int last = total == S;
+        if (last) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
         sm.is_last = last;
+        sm.foreign = (old & ~(127ull << (7 * x))) != 0ull;
     }
     __syncthreads();
     return sm.is_last != 0;
@@ -1795,23 +1819,52 @@ __device__ __forceinline__ bool nucleus_from_cands(const DevGroup& G, const Ctx&
     return true;
 }
 
+// The max, first argmax and full normaliser of the row straight from its logits (no published data), for a row
+// whose slices did not all run on the finaliser's XCD.  An all -inf row answers index 0, like the slice path.
+template <int ES>
+__device__ __forceinline__ void stream_stats(const DevGroup& G, const Ctx& c, Smem& sm, float& m, int& am, double& z) {
+    float mx = -INFINITY;
+    int ai = INT_MAX;
+    visit_row<ES>(G, c, sm, [&](float f, int j) {
+        if (f > mx) {
+            mx = f;
+            ai = j;
+        }
+    });
+    m = block_max(mx, sm);
+    am = block_min_i(m > -INFINITY && mx == m ? ai : INT_MAX, sm);
+    if (am == INT_MAX) am = 0;
+    double zpart = 0.0;
+    if (m > -INFINITY)
+        visit_row<ES>(G, c, sm, [&](float f, int) {
+            if (finite_f(f)) zpart += (double)expf(f - m);
+        });
+    z = block_sum_d(zpart, sm);
+}
+
 template <int ES>
 __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
     constexpr int E = 16 / ES;
     constexpr int NSB = kNV / E * kWaves;
-    load_summaries<ES>(c, sm, w);
     float m = -INFINITY, gmax = -INFINITY;
     double z = 0.0;
     int am = INT_MAX, ntot = 0;
     bool overflow = false;
-    for (int s = 0; s < c.S; ++s) m = fmaxf(m, sm.summ[s].m);
-    for (int s = 0; s < c.S; ++s) {
-        const SliceSummary& q = sm.summ[s];
-        if (q.m == m && q.argmax < am) am = q.argmax;
-        if (q.m > -INFINITY) z += q.z * exp((double)q.m - (double)m);
-        gmax = fmaxf(gmax, q.g);
-        ntot += q.ncand;
-        overflow |= q.overflow != 0;
+    // no published data: everything below streams the row
+    const bool foreign = sm.foreign != 0 || (G.flags & MIS_FINALIZE_STREAMING) != 0;
+    if (foreign) {
+        stream_stats<ES>(G, c, sm, m, am, z);
+    } else {
+        load_summaries<ES>(c, sm, w);
+        for (int s = 0; s < c.S; ++s) m = fmaxf(m, sm.summ[s].m);
+        for (int s = 0; s < c.S; ++s) {
+            const SliceSummary& q = sm.summ[s];
+            if (q.m == m && q.argmax < am) am = q.argmax;
+            if (q.m > -INFINITY) z += q.z * exp((double)q.m - (double)m);
+            gmax = fmaxf(gmax, q.g);
+            ntot += q.ncand;
+            overflow |= q.overflow != 0;
+        }
     }
     Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
     const bool drop_eos = c.hf && c.censor;
@@ -1822,7 +1875,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
         tok = am == INT_MAX ? c.V - 1 : am;
     } else if (!(m > -INFINITY)) {
         tok = c.V - 1;  // nothing allowed: the reference's clamp value
-    } else if (c.full_draw) {
+    } else if (c.full_draw && !foreign) {
         if (need_tok) {
             // survivors = every finite value (minus a censored EOS): the published sub-block sums
             const int nsb = c.S * NSB;
@@ -1844,7 +1897,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
             }
             tok = sub_block_draw<ES>(G, c, sm, nsb, -INFINITY, m, drop_eos, row_uniform(G, c));
         }
-    } else if (c.cand_mode && !overflow && ntot <= kCapRow) {
+    } else if (c.cand_mode && !foreign && !overflow && ntot <= kCapRow) {
         // candidates of all slices in vocabulary order; keys of those >= gmax
         int nge = 0;
         const int np = gather_cands(c, sm, w, ntot, gmax, nge);
@@ -1856,9 +1909,10 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
         } else {
             tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
         }
-    } else if (c.nucleus && nucleus_from_cands(G, c, sm, w, ntot, overflow, gmax, m, z, drop_eos, need_tok, thr, tok)) {
+    } else if (c.nucleus && !foreign &&
+               nucleus_from_cands(G, c, sm, w, ntot, overflow, gmax, m, z, drop_eos, need_tok, thr, tok)) {
         // resolved from the published candidates
-    } else if (c.nucleus) {
+    } else if (c.nucleus && !foreign) {
         // merge the slices' mass histograms on the global 1/8-logit grid, below the row's top bin
         const int HB = bin_of(m);
         double gm = 0.0;
@@ -2026,6 +2080,8 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
     if (c.S > 1) {
         if (!arrive_last(G.counters + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
     } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
+        if (threadIdx.x == 0) sm.foreign = 0;
         __syncthreads();
     }
     finalize<ES>(G, c, sm, w);
@@ -2071,10 +2127,13 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     if (c.S > 1) {
         if (!arrive_last(G.counters + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
     } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
+        if (threadIdx.x == 0) sm.foreign = 0;
         __syncthreads();
     }
-    // ---- finalise: exact top-p inside the boundary bin, then the draw
-    load_summaries<ES>(c, sm, w);
+    // ---- finalise: exact top-p inside the boundary bin, then the draw (a row split across XCDs streams instead)
+    const bool foreign = sm.foreign != 0;
+    if (!foreign) load_summaries<ES>(c, sm, w);
     const float m = P.m;
     const bool drop_eos = c.hf && c.censor;
     int ntot = 0, nabove = 0;
@@ -2088,7 +2147,7 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     }
     float thr = -INFINITY;
     int64_t tok = kPad;
-    bool exact = !overflow && ntot <= kCapRow && ntot > 0 && above < P.target;
+    bool exact = !foreign && !overflow && ntot <= kCapRow && ntot > 0 && above < P.target;
     if (exact) {
         int nkeys = 0;
         const int np = gather_cands(c, sm, w, ntot, -INFINITY, nkeys);
@@ -2142,6 +2201,7 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
                 v = fmax(0.0, v - (double)expf(fe - m));
             pub_st(&w.sb[(int64_t)s * kMaxSB + sb], v);  // staged in global memory: LDS still holds the candidates
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // in the L2 before other threads read them back
         __syncthreads();
         for (int i = threadIdx.x; i < nsb; i += kBlock) sm.u.sbs[i] = pub_ld(&w.sb[(int64_t)(i / NSB) * kMaxSB + i % NSB]);
         __syncthreads();
@@ -2152,18 +2212,26 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
 }
 
 __device__ __forceinline__ bool locate(const KernelArgs& args, int& gi, int& row, int& slice) {
-    const int bid = blockIdx.x;
-    const int w = (bid % 8) * args.per_xcd + bid / 8;  // consecutive work items (a row's slices) share an XCD
-    if (w >= args.total_blocks) return false;
-    gi = 0;
-    while (gi + 1 < args.n_groups && w >= args.g[gi + 1].block_begin) ++gi;
-    const int local = w - args.g[gi].block_begin;
-    row = local / args.g[gi].slices;
-    slice = local % args.g[gi].slices;
-    return true;
+    const int x = blockIdx.x % 8;
+    int i = blockIdx.x / 8;
+    for (gi = 0; gi < args.n_groups; ++gi) {
+        const int S = args.g[gi].slices;
+        const int n = args.seg_rows[x][gi] * S;
+        if (i < n) {
+            row = args.seg_row[x][gi] + i / S;
+            slice = i % S;
+            return true;
+        }
+        i -= n;
+    }
+    return false;
 }
 
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(const KernelArgs args) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(const KernelArgs args_in) {
+    // the arguments are read in place through the kernarg segment (indexing the by-value parameter with a
+    // run-time group index can make the compiler copy all of it to scratch)
+    (void)args_in;
+    const KernelArgs& args = *(const KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     __shared__ Smem sm;
     int gi, row, slice;
     if (!locate(args, gi, row, slice)) return;
@@ -2176,7 +2244,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
 
 // The nucleus pass over the sample kernel's grid: the workgroups of rows with a pending record redo their slice
 // and resolve the row; every other workgroup leaves after reading that record.
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args_in) {
+    // the arguments are read in place through the kernarg segment (indexing the by-value parameter with a
+    // run-time group index can make the compiler copy all of it to scratch)
+    (void)args_in;
+    const KernelArgs& args = *(const KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     __shared__ Smem sm;
     int gi, row, slice;
     if (!locate(args, gi, row, slice)) return;
@@ -2359,8 +2431,20 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     if (ws_off > workspace_bytes || (ws_off > 0 && !workspace))
         return fail(MIS_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", ws_off, workspace_bytes);
     if (blocks == 0) return 0;
-    a.total_blocks = blocks;
-    a.per_xcd = (blocks + 7) / 8;
+    // whole rows to XCDs: contiguous in (group, row) order, balanced by slice count
+    int64_t count[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t prefix = 0;
+    for (int gi = 0; gi < n_groups; ++gi) {
+        const int S = a.g[gi].slices;
+        for (int r = 0; r < groups[gi].rows; ++r) {
+            const int x = (int)std::min<int64_t>(7, ((prefix + S / 2) * 8) / blocks);
+            if (a.seg_rows[x][gi] == 0) a.seg_row[x][gi] = r;
+            ++a.seg_rows[x][gi];
+            count[x] += S;
+            prefix += S;
+        }
+    }
+    a.per_xcd = (int)*std::max_element(count, count + 8);
     const int grid = a.per_xcd * 8;
     hipLaunchKernelGGL(sample_kernel, dim3(grid), dim3(kBlock), 0, (hipStream_t)stream, a);
     hipError_t e = hipGetLastError();

@@ -19,7 +19,7 @@ MIS_F32, MIS_BF16 = 0, 1
 MIS_OMNI, MIS_HF = 0, 1
 MIS_RNG_COUNTER, MIS_RNG_PHILOX = 0, 1
 MIS_HISTORY_WINDOW, MIS_HISTORY_RING = 0, 1
-MIS_TOPK_ZERO_DISABLES, MIS_TOPP_ONE_DISABLES, MIS_UPDATE_STATE = 1, 2, 4
+MIS_TOPK_ZERO_DISABLES, MIS_TOPP_ONE_DISABLES, MIS_UPDATE_STATE, MIS_FINALIZE_STREAMING = 1, 2, 4, 8
 MIS_E_ARG, MIS_E_WORKSPACE, MIS_E_UNSUPPORTED = 1, 2, 3
 
 _vp = ctypes.c_void_p

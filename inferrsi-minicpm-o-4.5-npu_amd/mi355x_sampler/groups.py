@@ -47,7 +47,7 @@ class RowGroup:
                  active: torch.Tensor | None = None, finished: torch.Tensor | None = None, semantics: str = "omni",
                  min_keep: int = 1, rng: str = "counter", top_k_zero_disables: bool = True,
                  top_p_one_disables: bool = True, update_state: bool = False, tokens=True, processed=False,
-                 probs=False, alpha_lut: torch.Tensor | None = None):
+                 probs=False, alpha_lut: torch.Tensor | None = None, finalize_streaming: bool = False):
         if not isinstance(logits, torch.Tensor) or logits.dim() != 2:
             raise ValueError("logits must be a [rows, vocab] tensor")
         self.device = logits.device
@@ -71,7 +71,8 @@ class RowGroup:
         g.min_keep = int(min_keep)
         g.flags = ((_lib.MIS_TOPK_ZERO_DISABLES if top_k_zero_disables else 0)
                    | (_lib.MIS_TOPP_ONE_DISABLES if top_p_one_disables else 0)
-                   | (_lib.MIS_UPDATE_STATE if update_state else 0))
+                   | (_lib.MIS_UPDATE_STATE if update_state else 0)
+                   | (_lib.MIS_FINALIZE_STREAMING if finalize_streaming else 0))
         g.temperature, g.temperature_value = self._param(temperature, torch.float32, "temperature")
         g.top_k, g.top_k_value = self._param(top_k, torch.int32, "top_k")
         g.top_p, g.top_p_value = self._param(top_p, torch.float32, "top_p")

@@ -65,6 +65,47 @@ def test_workload_matches_oracle(name, make):
     assert stats["exact"] >= wl.rows - max(1, wl.rows // 16)
 
 
+STREAMING = [
+    ("talker_b8_hf", lambda: W.talker_b8("hf")),
+    ("thinker_b8", lambda: W.thinker_b8()),
+    ("thinker_b8_greedy", lambda: W.thinker_b8(greedy=True)),
+]
+
+
+@pytest.mark.parametrize("name,make", STREAMING, ids=[n for n, _ in STREAMING])
+def test_streaming_finalise_matches_oracle(name, make):
+    """The finaliser a row takes when its slices did not share an XCD: from the logits alone."""
+    wl = make()
+    print(f"[gpu] streaming finalise {name}", flush=True)
+    g = run(wl, finalize_streaming=True)
+    rows = oracle_rows(wl)
+    ref = ext.sample_rows(rows)
+    stats = compare_group(name, g.tokens, g.processed, g.probs, ref, rows,
+                          prob_rtol=1e-5 if wl.logits.dtype == torch.float32 else 2e-3)
+    print(f"[gpu] streaming {name}: {stats}", flush=True)
+    assert stats["exact"] >= wl.rows - max(1, wl.rows // 16)
+
+
+@pytest.mark.parametrize("rows", [1, 3, 5, 9, 13])
+def test_row_counts_that_do_not_fill_xcds_evenly(rows):
+    """Batches whose slices do not divide evenly over the eight XCDs: every row still sees only its own slices."""
+    print(f"[gpu] uneven rows={rows}", flush=True)
+    x = torch.randn(rows, W.THINKER_V, generator=torch.Generator().manual_seed(77 + rows)).to(DEV)
+    for _ in range(2):  # twice: a stale slot from the first launch must not leak into the second
+        got = G.greedy(x)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), torch.argmax(x.cpu(), dim=-1))
+    g = G.RowGroup(x, temperature=0.9, top_k=50, top_p=0.9, seeds=torch.full((rows,), 5, device=DEV),
+                   steps=torch.zeros(rows, dtype=torch.int64, device=DEV), processed=True, probs=True)
+    G.launch([g])
+    torch.cuda.synchronize()
+    one = lambda v, dt=torch.float32: torch.full((rows,), v, dtype=dt)  # noqa: E731
+    ref_rows = ext.Rows(logits=x.cpu(), temperature=one(0.9), top_k=one(50, torch.int32), top_p=one(0.9),
+                        repetition=one(1.0), presence=one(0.0), frequency=one(0.0), seeds=one(5, torch.int64),
+                        steps=one(0, torch.int64))
+    compare_group(f"uneven{rows}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows, prob_rtol=1e-5)
+
+
 def test_thinker_greedy_is_first_argmax_at_full_size():
     wl = W.thinker_b64().to(DEV)
     x = wl.logits.clone()
