@@ -127,6 +127,13 @@ struct DevGroup {
     int64_t ws_row_bytes;
 };
 
+// A pointer into global memory as such: accesses through it compile to global (not flat) instructions, which
+// count only against the vector-memory counter.
+template <class T>
+__device__ __forceinline__ T* gp(T* p) {
+    return (T*)(__attribute__((address_space(1))) T*)p;
+}
+
 // Whole rows are assigned to XCDs: block b runs on XCD b % 8 (the dispatcher's round-robin), as the (b / 8)-th
 // slice of that XCD's rows, which are rows [seg_row[x][g], + seg_rows[x][g]) of each group g in turn.
 struct KernelArgs {
@@ -316,8 +323,109 @@ __device__ __forceinline__ SliceSummary pub_ld_summary(const SliceSummary* d) {
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// threadIdx.x through an opaque copy: index arithmetic derived from it is recomputed where it is used instead of
+// being shared with (and kept live from) an earlier phase.
+__device__ __forceinline__ int fresh_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+__device__ __forceinline__ int fresh_lane() { return fresh_tid() & 63; }
+
+// Cross-lane moves.  Each computes its own lane arithmetic, so no lane index is shared (and kept live) across the
+// kernel: xor offsets below 32 use ds_swizzle's bit-mask mode (the pattern is an immediate), the others
+// ds_bpermute.
+template <int O>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t x) {
+    static_assert(O >= 1 && O <= 32 && (O & (O - 1)) == 0, "power-of-two offset");
+    if constexpr (O == 32)
+        return (uint32_t)__builtin_amdgcn_ds_bpermute((fresh_lane() ^ 32) << 2, (int)x);
+    else
+        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1f | (O << 10));  // lane ^ O within 32 lanes
+}
+
+__device__ __forceinline__ uint32_t xor_lane_dyn(uint32_t x, int o) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute((fresh_lane() ^ o) << 2, (int)x);
+}
+
+// lane l receives lane l - o (lanes below o receive a lane of the upper half; callers ignore them)
+__device__ __forceinline__ uint32_t up_lane(uint32_t x, int o) {
+    return (uint32_t)__builtin_amdgcn_ds_bpermute(((fresh_lane() - o) & 63) << 2, (int)x);
+}
+
+template <class T>
+struct Lanes;  // moves a value through 32-bit lane moves
+template <>
+struct Lanes<uint32_t> {
+    template <class F>
+    __device__ static uint32_t mv(uint32_t x, F f) { return f(x); }
+};
+template <>
+struct Lanes<int> {
+    template <class F>
+    __device__ static int mv(int x, F f) { return (int)f((uint32_t)x); }
+};
+template <>
+struct Lanes<float> {
+    template <class F>
+    __device__ static float mv(float x, F f) { return __uint_as_float(f(__float_as_uint(x))); }
+};
+template <>
+struct Lanes<unsigned long long> {
+    template <class F>
+    __device__ static unsigned long long mv(unsigned long long x, F f) {
+        return ((unsigned long long)f((uint32_t)(x >> 32)) << 32) | f((uint32_t)x);
+    }
+};
+template <>
+struct Lanes<double> {
+    template <class F>
+    __device__ static double mv(double x, F f) {
+        return __longlong_as_double((long long)Lanes<unsigned long long>::mv((unsigned long long)__double_as_longlong(x), f));
+    }
+};
+
+template <int O, class T>
+__device__ __forceinline__ T shfl_xor_c(T x) {
+    return Lanes<T>::mv(x, [](uint32_t v) { return xor_lane<O>(v); });
+}
+
+template <class T>
+__device__ __forceinline__ T shfl_xor_d(T x, int o) {
+    return Lanes<T>::mv(x, [o](uint32_t v) { return xor_lane_dyn(v, o); });
+}
+
+template <class T>
+__device__ __forceinline__ T shfl_up_d(T x, int o) {
+    return Lanes<T>::mv(x, [o](uint32_t v) { return up_lane(v, o); });
+}
+
+// All 64 lanes end with op over the wave (a symmetric butterfly: every lane computes the same sums).
+template <class T, class Op>
+__device__ __forceinline__ T wave_reduce(T x, Op op) {
+    x = op(x, shfl_xor_c<32>(x));
+    x = op(x, shfl_xor_c<16>(x));
+    x = op(x, shfl_xor_c<8>(x));
+    x = op(x, shfl_xor_c<4>(x));
+    x = op(x, shfl_xor_c<2>(x));
+    x = op(x, shfl_xor_c<1>(x));
+    return x;
+}
+
+// Inclusive scan over the wave's lanes.
+template <class T>
+__device__ __forceinline__ T wave_incl_scan(T x) {
+    const int l = lane_id();
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T y = shfl_up_d(x, o);
+        if (l >= o) x += y;
+    }
+    return x;
+}
+
 __device__ __forceinline__ float block_max(float x, Smem& sm) {
-    for (int o = 32; o; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    x = wave_reduce(x, [](float a, float b) { return fmaxf(a, b); });
     __syncthreads();
     if (lane_id() == 0) sm.red_f[wave_id()] = x;
     __syncthreads();
@@ -327,7 +435,7 @@ __device__ __forceinline__ float block_max(float x, Smem& sm) {
 }
 
 __device__ __forceinline__ int block_min_i(int x, Smem& sm) {
-    for (int o = 32; o; o >>= 1) x = min(x, __shfl_xor(x, o));
+    x = wave_reduce(x, [](int a, int b) { return min(a, b); });
     __syncthreads();
     if (lane_id() == 0) sm.red_i[wave_id()] = x;
     __syncthreads();
@@ -337,7 +445,7 @@ __device__ __forceinline__ int block_min_i(int x, Smem& sm) {
 }
 
 __device__ __forceinline__ int block_max_i(int x, Smem& sm) {
-    for (int o = 32; o; o >>= 1) x = max(x, __shfl_xor(x, o));
+    x = wave_reduce(x, [](int a, int b) { return max(a, b); });
     __syncthreads();
     if (lane_id() == 0) sm.red_i[wave_id()] = x;
     __syncthreads();
@@ -347,7 +455,7 @@ __device__ __forceinline__ int block_max_i(int x, Smem& sm) {
 }
 
 __device__ __forceinline__ int block_sum_i(int x, Smem& sm) {
-    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    x = wave_reduce(x, [](int a, int b) { return a + b; });
     __syncthreads();
     if (lane_id() == 0) sm.red_i[wave_id()] = x;
     __syncthreads();
@@ -357,8 +465,12 @@ __device__ __forceinline__ int block_sum_i(int x, Smem& sm) {
 }
 
 // Fixed reduction tree: the result does not depend on scheduling.
+__device__ __forceinline__ double wave_sum_d(double x) {
+    return wave_reduce(x, [](double a, double b) { return a + b; });
+}
+
 __device__ __forceinline__ double block_sum_d(double x, Smem& sm) {
-    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    x = wave_sum_d(x);
     __syncthreads();
     if (lane_id() == 0) sm.red_d[wave_id()] = x;
     __syncthreads();
@@ -368,7 +480,7 @@ __device__ __forceinline__ double block_sum_d(double x, Smem& sm) {
 }
 
 __device__ __forceinline__ unsigned long long block_sum_u(unsigned long long x, Smem& sm) {
-    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
+    x = wave_reduce(x, [](unsigned long long a, unsigned long long b) { return a + b; });
     __syncthreads();
     if (lane_id() == 0) sm.red_u[wave_id()] = x;
     __syncthreads();
@@ -377,19 +489,10 @@ __device__ __forceinline__ unsigned long long block_sum_u(unsigned long long x, 
     return r;
 }
 
-__device__ __forceinline__ double wave_sum_d(double x) {
-    for (int o = 32; o; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
-
 // Exclusive prefix from the lane-shifted inclusive scan (no subtraction).
 __device__ __forceinline__ double block_excl_scan_d(double x, double& total, Smem& sm) {
-    double incl = x;
-    for (int o = 1; o < 64; o <<= 1) {
-        const double y = __shfl_up(incl, o);
-        if (lane_id() >= o) incl += y;
-    }
-    double excl = __shfl_up(incl, 1);
+    const double incl = wave_incl_scan(x);
+    double excl = shfl_up_d(incl, 1);
     if (lane_id() == 0) excl = 0.0;
     __syncthreads();
     if (lane_id() == 63) sm.red_d[wave_id()] = incl;
@@ -405,11 +508,7 @@ __device__ __forceinline__ double block_excl_scan_d(double x, double& total, Sme
 
 __device__ __forceinline__ unsigned long long block_excl_scan_u(unsigned long long x, unsigned long long& total,
                                                                Smem& sm) {
-    unsigned long long incl = x;
-    for (int o = 1; o < 64; o <<= 1) {
-        const unsigned long long y = __shfl_up(incl, o);
-        if (lane_id() >= o) incl += y;
-    }
+    const unsigned long long incl = wave_incl_scan(x);
     __syncthreads();
     if (lane_id() == 63) sm.red_u[wave_id()] = incl;
     __syncthreads();
@@ -442,23 +541,66 @@ struct Ctx {
     int cand_target;   // per-slice candidate count target
 };
 
-__device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, Ctx& c) {
+// A row's parameters as loaded; the loads are issued before the slice's tile so that waiting for them does not
+// wait for the tile (vector loads complete in order).
+struct RowParams {
+    int64_t step;
+    float t, p, rep, pres, freq;
+    int k;
+    uint8_t act, fin;
+};
+
+// Row-uniform values into scalar registers (they arrive from vector loads).
+__device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ float uni(float x) { return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x))); }
+__device__ __forceinline__ int64_t uni(int64_t x) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x), hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ void load_params(const DevGroup& G, int row, RowParams& q) {
+    q.step = gp(G.steps) ? gp(G.steps)[row] : 0;
+    q.t = gp(G.temperature) ? gp(G.temperature)[row] : G.t_val;
+    q.p = gp(G.top_p) ? gp(G.top_p)[row] : G.p_val;
+    q.rep = gp(G.repetition) ? gp(G.repetition)[row] : G.rep_val;
+    q.pres = gp(G.presence) ? gp(G.presence)[row] : G.pres_val;
+    q.freq = gp(G.frequency) ? gp(G.frequency)[row] : G.freq_val;
+    q.k = gp(G.top_k) ? gp(G.top_k)[row] : G.k_val;
+    q.act = gp(G.active) ? gp(G.active)[row] : (uint8_t)1;
+    q.fin = gp(G.finished) ? gp(G.finished)[row] : (uint8_t)0;
+}
+
+// The loaded parameters, once they are needed, as scalars.
+__device__ __forceinline__ void settle_params(RowParams& q) {
+    q.step = uni(q.step);
+    q.t = uni(q.t);
+    q.p = uni(q.p);
+    q.rep = uni(q.rep);
+    q.pres = uni(q.pres);
+    q.freq = uni(q.freq);
+    q.k = uni(q.k);
+    q.act = (uint8_t)uni((int)q.act);
+    q.fin = (uint8_t)uni((int)q.fin);
+}
+
+__device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, RowParams q, Ctx& c) {
+    settle_params(q);
     c.row = row;
     c.slice = slice;
     c.grow = G.row_begin + row;
     c.S = G.slices;
     c.V = G.vocab;
     c.slice_len = G.slice_len;
-    c.step = G.steps ? G.steps[row] : 0;
-    const float t = G.temperature ? G.temperature[row] : G.t_val;
+    c.step = q.step;
+    const float t = q.t;
     c.greedy = !(t > 0.f);
     c.tdiv = c.greedy ? 1.0f : t;
     c.rtdiv = 1.0f / c.tdiv;
-    c.top_p = G.top_p ? G.top_p[row] : G.p_val;
-    c.rep = G.repetition ? G.repetition[row] : G.rep_val;
-    c.pres = G.presence ? G.presence[row] : G.pres_val;
-    c.freq = G.frequency ? G.frequency[row] : G.freq_val;
-    const int k = G.top_k ? G.top_k[row] : G.k_val;
+    c.top_p = q.p;
+    c.rep = q.rep;
+    c.pres = q.pres;
+    c.freq = q.freq;
+    const int k = q.k;
     if ((G.flags & MIS_TOPK_ZERO_DISABLES) && k <= 0)
         c.k_eff = c.V;
     else
@@ -469,12 +611,10 @@ __device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, 
     c.later = c.step > 0;
     c.censor = G.eos >= 0 && c.step < (int64_t)G.min_new;
     c.forced = G.eos >= 0 && G.max_new > 0 && c.step >= (int64_t)G.max_new - 1;
-    const bool act = G.active ? G.active[row] != 0 : true;
-    const bool fin = G.finished ? G.finished[row] != 0 : false;
-    c.live = act && !fin;
-    c.want_out = G.processed != nullptr || G.probs != nullptr;
-    const bool pen = G.hist_len > 0 && G.history != nullptr &&
-                     (c.rep != 1.0f || c.pres != 0.0f || c.freq != 0.0f || G.alpha_lut != nullptr);
+    c.live = q.act != 0 && q.fin == 0;
+    c.want_out = gp(G.processed) != nullptr || gp(G.probs) != nullptr;
+    const bool pen = G.hist_len > 0 && gp(G.history) != nullptr &&
+                     (c.rep != 1.0f || c.pres != 0.0f || c.freq != 0.0f || gp(G.alpha_lut) != nullptr);
     c.counts = pen && (!c.hf || c.later);
     const bool filters = !c.greedy && (!c.hf || c.later);
     c.full_draw = !c.greedy && (!filters || (c.k_eff >= c.V && !c.p_active));
@@ -486,12 +626,18 @@ __device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, 
     c.need_mass = c.full_draw || c.nucleus || (c.hf && filters && c.p_active);
 }
 
+__device__ __forceinline__ void init_ctx(const DevGroup& G, int row, int slice, Ctx& c) {
+    RowParams q;
+    load_params(G, row, q);
+    init_ctx(G, row, slice, q, c);
+}
+
 // ---------------------------------------------------------------- the element pipeline
 
 // rep**n by binary powering in double (<= 32 products, relative error < 4e-15) rounded once to float, or the
 // caller's table where it covers n.
 __device__ __forceinline__ float alpha_exact(const DevGroup& G, float rep, int n) {
-    if (G.alpha_lut != nullptr && n < G.alpha_lut_len) return G.alpha_lut[n];
+    if (gp(G.alpha_lut) != nullptr && n < G.alpha_lut_len) return gp(G.alpha_lut)[n];
     double r = 1.0, b = (double)rep;
     for (unsigned e = (unsigned)n; e; e >>= 1) {
         if (e & 1u) r *= b;
@@ -584,7 +730,7 @@ __device__ __forceinline__ int clear_counts(const DevGroup& G, const Ctx& c, int
 }
 
 __device__ __forceinline__ const char* hist_row(const DevGroup& G, int row) {
-    return G.history + (int64_t)row * G.hist_stride * (G.hist_i64 ? 8 : 4);
+    return gp(G.history) + (int64_t)row * G.hist_stride * (G.hist_i64 ? 8 : 4);
 }
 
 // int32 ids, 16-byte aligned rows, W % 4 == 0: the history is read as int4.
@@ -658,7 +804,7 @@ __device__ __forceinline__ Geo slice_geo_at(const DevGroup& G, int row, int s) {
     Geo g;
     g.lo = s * G.slice_len;
     g.hi = min(G.vocab, g.lo + G.slice_len);
-    const char* rowp = G.logits + (int64_t)row * G.row_stride * ES;
+    const char* rowp = gp(G.logits) + (int64_t)row * G.row_stride * ES;
     const uintptr_t lo_addr = (uintptr_t)(rowp + (int64_t)g.lo * ES);
     g.base = lo_addr & ~(uintptr_t)15;
     g.first = g.lo - (int)((lo_addr - g.base) / ES);
@@ -735,17 +881,19 @@ struct Preload {
 };
 
 __device__ __forceinline__ void preload(const DevGroup& G, int row, const Geo& g, Preload& P) {
-    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)row * G.allowed_stride : nullptr;
+    const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)row * G.allowed_stride : nullptr;
     const int wb = g.first >> 5;  // arithmetic shift: first may be negative in slice 0
+    const int wmax = (G.vocab - 1) >> 5;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int gw = wb + (int)threadIdx.x + u * kBlock;
         const int a = g.lo - 32 * gw, b = g.hi - 32 * gw;
         uint32_t m = (a <= 0 ? ~0u : a >= 32 ? 0u : ~0u << a) & (b >= 32 ? ~0u : b <= 0 ? 0u : (1u << b) - 1u);
-        if (m != 0u && mrow != nullptr) m &= mrow[gw];  // m != 0: word gw meets [lo, hi), inside the row
+        // unconditional load of a clamped word (words outside [lo, hi) are masked off by m anyway)
+        if (mrow != nullptr) m &= mrow[min(max(gw, 0), wmax)];
         P.mw[u] = m;
     }
-    const char* hrow = G.history != nullptr && G.hist_len > 0 ? hist_row(G, row) : nullptr;
+    const char* hrow = gp(G.history) != nullptr && G.hist_len > 0 ? hist_row(G, row) : nullptr;
     P.hvec = hrow != nullptr && hist_vec(G, hrow);
     if (P.hvec) {
         const int4* h4 = (const int4*)hrow;
@@ -807,9 +955,10 @@ __device__ __forceinline__ void process_tile_t(const DevGroup& G, const Ctx& c, 
     constexpr int NCH = kNV / E;
     const float d = c.tdiv, rd = c.rtdiv;
     const int wb = g.first >> 5;
+    const int tid = fresh_tid();
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
-        const int ch = threadIdx.x + kBlock * i;
+        const int ch = tid + kBlock * i;
         const int j0 = g.first + ch * E;
         const bool live = ch < g.nchunk;
         const int k = min((j0 >> 5) - wb, kMaskWords - 2);
@@ -1018,7 +1167,7 @@ __device__ __forceinline__ void stream_slice(const DevGroup& G, const Ctx& c, in
     constexpr int E = 16 / ES;
     const Geo g = slice_geo<ES>(G, c, s);
     if (c.counts) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
-    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+    const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)c.row * G.allowed_stride : nullptr;
     const int nwords = (c.V + 31) >> 5;
     for (int ch = threadIdx.x; ch < g.nchunk; ch += kBlock) {
         const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
@@ -1051,7 +1200,7 @@ __device__ __forceinline__ void pick_count_bin(int rem, Smem& sm) {
         }
         int incl = sum;
         for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
+            const int y = shfl_up_d(incl, o);
             if (l >= o) incl += y;
         }
         int before = incl - sum;
@@ -1135,7 +1284,7 @@ __device__ __forceinline__ float stream_mass(const DevGroup& G, const Ctx& c, Sm
             }
             unsigned long long incl = sum;
             for (int o = 1; o < 64; o <<= 1) {
-                const unsigned long long y = __shfl_up(incl, o);
+                const unsigned long long y = shfl_up_d(incl, o);
                 if (l >= o) incl += y;
             }
             unsigned long long before = acc + (incl - sum);
@@ -1149,7 +1298,7 @@ __device__ __forceinline__ float stream_mass(const DevGroup& G, const Ctx& c, Sm
                 before += hm[r];
             }
             int lowest = mine < 0 ? 1 << 20 : mine;
-            for (int o = 32; o; o >>= 1) lowest = min(lowest, __shfl_xor(lowest, o));
+            lowest = wave_reduce(lowest, [](int a, int b) { return min(a, b); });
             if (mine >= 0 && mine == lowest) {
                 sm.sel_bin = mine;
                 sm.sel_acc = mine_before;
@@ -1200,7 +1349,7 @@ __device__ __forceinline__ int stream_draw(const DevGroup& G, const Ctx& c, Smem
         constexpr int E = 16 / ES;
         const Geo g = slice_geo<ES>(G, c, s);
         if (c.counts) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
-        const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+        const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)c.row * G.allowed_stride : nullptr;
         const int nwords = (c.V + 31) >> 5;
         int found = INT_MAX;
         double run_base = base;
@@ -1291,9 +1440,9 @@ __device__ __forceinline__ float philox_uniform(int64_t seed, int64_t step, int6
 }
 
 __device__ __forceinline__ float row_uniform(const DevGroup& G, const Ctx& c) {
-    if (G.uniforms) return G.uniforms[c.row];
-    const int64_t seed = G.seeds ? G.seeds[c.row] : 0;
-    if (G.rng == MIS_RNG_PHILOX) return philox_uniform(seed, c.step, G.row_ids ? G.row_ids[c.row] : 0);
+    if (gp(G.uniforms)) return gp(G.uniforms)[c.row];
+    const int64_t seed = gp(G.seeds) ? gp(G.seeds)[c.row] : 0;
+    if (G.rng == MIS_RNG_PHILOX) return philox_uniform(seed, c.step, gp(G.row_ids) ? gp(G.row_ids)[c.row] : 0);
     return counter_uniform(seed, c.step);
 }
 
@@ -1303,8 +1452,8 @@ __device__ __forceinline__ float row_uniform(const DevGroup& G, const Ctx& c) {
 template <int ES>
 __device__ __forceinline__ void write_outputs(const DevGroup& G, const Ctx& c, Smem& sm, float thr, float m,
                                               bool drop_eos) {
-    float* prow = G.processed ? G.processed + (int64_t)c.row * G.processed_stride : nullptr;
-    float* qrow = G.probs ? G.probs + (int64_t)c.row * G.probs_stride : nullptr;
+    float* prow = gp(G.processed) ? gp(G.processed) + (int64_t)c.row * G.processed_stride : nullptr;
+    float* qrow = gp(G.probs) ? gp(G.probs) + (int64_t)c.row * G.probs_stride : nullptr;
     if (c.forced) {
         for (int j = threadIdx.x; j < c.V; j += kBlock) {
             const bool e = j == G.eos;
@@ -1330,20 +1479,20 @@ __device__ __forceinline__ void write_outputs(const DevGroup& G, const Ctx& c, S
 // tokens[row]; for live rows with MIS_UPDATE_STATE: history append, steps + 1, finished |= (token == eos).
 __device__ __forceinline__ void update_state(const DevGroup& G, const Ctx& c, int64_t tok) {
     if (!(G.flags & MIS_UPDATE_STATE) || !c.live) {
-        if (threadIdx.x == 0 && G.tokens) G.tokens[c.row] = c.live ? tok : kPad;
+        if (threadIdx.x == 0 && gp(G.tokens)) gp(G.tokens)[c.row] = c.live ? tok : kPad;
         return;
     }
-    if (G.history && G.hist_len > 0) {
+    if (gp(G.history) && G.hist_len > 0) {
         const int W = G.hist_len;
-        char* hrow = (char*)G.history + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
+        char* hrow = (char*)gp(G.history) + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
         if (G.hist_mode == MIS_HISTORY_RING) {
             if (threadIdx.x == 0) {
-                const int pos = (int)((G.hist_head[c.row] % W + W) % W);
+                const int pos = (int)((gp(G.hist_head)[c.row] % W + W) % W);
                 if (G.hist_i64)
                     ((int64_t*)hrow)[pos] = tok;
                 else
                     ((int32_t*)hrow)[pos] = (int32_t)tok;
-                G.hist_head[c.row] = (pos + 1) % W;
+                gp(G.hist_head)[c.row] = (pos + 1) % W;
             }
         } else {
             // shift left by one, append: each round reads [b+1, b+kBlock] before writing [b, b+kBlock)
@@ -1368,9 +1517,9 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Ctx& c, in
         }
     }
     if (threadIdx.x == 0) {
-        if (G.tokens) G.tokens[c.row] = tok;
-        if (G.steps) G.steps[c.row] = c.step + 1;
-        if (G.finished && tok == (int64_t)G.eos) G.finished[c.row] = 1;
+        if (gp(G.tokens)) gp(G.tokens)[c.row] = tok;
+        if (gp(G.steps)) gp(G.steps)[c.row] = c.step + 1;
+        if (gp(G.finished) && tok == (int64_t)G.eos) gp(G.finished)[c.row] = 1;
     }
 }
 
@@ -1497,7 +1646,7 @@ __device__ __forceinline__ void sort_keys_desc(Smem& sm, int np) {
                     for (int r = 0; r < 8; ++r) b[r] = sm.u.c.key[(8 * t + r) ^ j];
                 } else {
 #pragma unroll
-                    for (int r = 0; r < 8; ++r) b[r] = __shfl_xor(a[r], j >> 3);
+                    for (int r = 0; r < 8; ++r) b[r] = shfl_xor_d(a[r], j >> 3);
                 }
                 // j >= 8 and k > j: both bits come from the lane, not from r
                 const bool keep_max = (((8 * t) & j) == 0) == (((8 * t) & k) == 0);
@@ -1610,7 +1759,7 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
     if ((int)threadIdx.x == owner) sm.red_d[0] = before;
     __syncthreads();
     before = owner >= 0 ? sm.red_d[0] : 0.0;
-    const uint32_t* mrow = G.allowed ? G.allowed + (int64_t)c.row * G.allowed_stride : nullptr;
+    const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)c.row * G.allowed_stride : nullptr;
     const int nwords = (c.V + 31) >> 5;
     int cur_slice = -1;
     for (int sbi = (first == INT_MAX ? nsb_total : first); sbi < nsb_total; ++sbi) {
@@ -1649,12 +1798,12 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
             // wave-level exclusive scan
             double incl = mine2;
             for (int o = 1; o < 64; o <<= 1) {
-                const double y = __shfl_up(incl, o);
+                const double y = shfl_up_d(incl, o);
                 if (lane_id() >= o) incl += y;
             }
             double r = before + incl - mine2;
             (void)r;
-            double ex = __shfl_up(incl, 1);
+            double ex = shfl_up_d(incl, 1);
             if (lane_id() == 0) ex = 0.0;
             double rr = before + ex;
 #pragma unroll
@@ -1663,7 +1812,7 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
                     rr += (double)pv[e];
                     if ((float)rr > target && found == INT_MAX) found = jv[e];
                 }
-            sbsum = __shfl(incl, 63);
+            sbsum = __longlong_as_double((long long)(((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)((unsigned long long)__double_as_longlong(incl) >> 32), 63) << 32) | (uint32_t)__builtin_amdgcn_readlane((int)__double_as_longlong(incl), 63)));
         }
         const int tok = block_min_i(found, sm);
         if (tok != INT_MAX) return tok;
@@ -1693,7 +1842,7 @@ __device__ __forceinline__ int gather_cands(const Ctx& c, Smem& sm, const RowWs&
         const int x = l < c.S ? sm.summ[l].ncand : 0;
         int incl = x;
         for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o);
+            const int y = shfl_up_d(incl, o);
             if (l >= o) incl += y;
         }
         sm.coff[l] = incl - x;
@@ -1771,21 +1920,21 @@ template <int ES>
 __device__ __forceinline__ float eos_value(const DevGroup& G, const Ctx& c, Smem& sm) {
     int n = 0;
     if (c.counts) {
-        const char* hrow = G.history + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
+        const char* hrow = gp(G.history) + (int64_t)c.row * G.hist_stride * (G.hist_i64 ? 8 : 4);
         for (int i = threadIdx.x; i < G.hist_len; i += kBlock) {
             const int64_t h = G.hist_i64 ? ((const int64_t*)hrow)[i] : (int64_t)((const int32_t*)hrow)[i];
             n += h == (int64_t)G.eos;
         }
         n = block_sum_i(n, sm);
     }
-    const char* rowp = G.logits + (int64_t)c.row * G.row_stride * ES;
+    const char* rowp = gp(G.logits) + (int64_t)c.row * G.row_stride * ES;
     float x;
     if (ES == 2)
         x = __uint_as_float((uint32_t)(*(const uint16_t*)(rowp + (int64_t)G.eos * 2)) << 16);
     else
         x = *(const float*)(rowp + (int64_t)G.eos * 4);
     bool allowed = true;
-    if (G.allowed) allowed = ((G.allowed[(int64_t)c.row * G.allowed_stride + (G.eos >> 5)] >> (G.eos & 31)) & 1u) != 0;
+    if (gp(G.allowed)) allowed = ((gp(G.allowed)[(int64_t)c.row * G.allowed_stride + (G.eos >> 5)] >> (G.eos & 31)) & 1u) != 0;
     return transform(x, G.eos, n, allowed, G, c, sm);
 }
 
@@ -1823,22 +1972,38 @@ __device__ __forceinline__ bool nucleus_from_cands(const DevGroup& G, const Ctx&
 // whose slices did not all run on the finaliser's XCD.  An all -inf row answers index 0, like the slice path.
 template <int ES>
 __device__ __forceinline__ void stream_stats(const DevGroup& G, const Ctx& c, Smem& sm, float& m, int& am, double& z) {
+    // max pass, then the first index of the max and the normaliser; plain loops over the row's 16-byte chunks
+    constexpr int E = 16 / ES;
     float mx = -INFINITY;
     int ai = INT_MAX;
-    visit_row<ES>(G, c, sm, [&](float f, int j) {
-        if (f > mx) {
-            mx = f;
-            ai = j;
-        }
-    });
-    m = block_max(mx, sm);
-    am = block_min_i(m > -INFINITY && mx == m ? ai : INT_MAX, sm);
-    if (am == INT_MAX) am = 0;
     double zpart = 0.0;
-    if (m > -INFINITY)
-        visit_row<ES>(G, c, sm, [&](float f, int) {
-            if (finite_f(f)) zpart += (double)expf(f - m);
-        });
+    for (int pass = 0; pass < 2; ++pass) {
+        if (pass == 1) m = block_max(mx, sm);
+        for (int s = 0; s < c.S; ++s) {
+            const Geo g = slice_geo<ES>(G, c, s);
+            if (c.counts) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
+            const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)c.row * G.allowed_stride : nullptr;
+            const int nwords = (c.V + 31) >> 5;
+            for (int ch = threadIdx.x; ch < g.nchunk; ch += kBlock) {
+                const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
+                const MaskPair mk = mrow ? mask_pair(mrow, nwords, g.first + ch * E) : MaskPair{~0u, ~0u, 0};
+                for (int e = 0; e < E; ++e) {
+                    const int j = g.first + ch * E + e;
+                    if (j < g.lo || j >= g.hi) continue;
+                    const int n = c.counts ? count_of(sm, j - g.first) : 0;
+                    const float f = transform(raw_elem<ES>(raw, e), j, n, mrow ? mask_bit(mk, j) : true, G, c, sm);
+                    if (pass == 0) {
+                        mx = fmaxf(mx, f);
+                    } else {
+                        if (f == m && j < ai) ai = j;
+                        if (finite_f(f)) zpart += (double)expf(f - m);
+                    }
+                }
+            }
+        }
+    }
+    am = m > -INFINITY ? block_min_i(ai, sm) : 0;  // an all -inf row answers index 0, like the slice path
+    if (am == INT_MAX) am = 0;
     z = block_sum_d(zpart, sm);
 }
 
@@ -1866,9 +2031,9 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
             overflow |= q.overflow != 0;
         }
     }
-    Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
+    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)c.grow * sizeof(Pending));
     const bool drop_eos = c.hf && c.censor;
-    const bool need_tok = G.tokens != nullptr || (G.flags & MIS_UPDATE_STATE);
+    const bool need_tok = gp(G.tokens) != nullptr || (G.flags & MIS_UPDATE_STATE);
     int64_t tok = kPad;
     float thr = -INFINITY;
     if (c.greedy) {
@@ -1976,22 +2141,23 @@ template <int ES>
 __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
     constexpr int E = 16 / ES;
     constexpr int NCH = kNV / E;
-    // the slice's loads go out before the row's parameters are read (those are scalar loads: they do not wait
-    // for the tile)
+    // the row's parameters, then the slice's tile, mask words and history go out before any of them is used
+    RowParams q;
+    load_params(G, row, q);
     const Geo geo = slice_geo_at<ES>(G, row, slice);
     RawTile<ES> R;
     issue_tile<ES>(geo, R);
     Preload P;
     preload(G, row, geo, P);
     Ctx c;
-    init_ctx(G, row, slice, c);
-    const RowWs w = row_ws(G.ws + (int64_t)row * G.ws_row_bytes, c.S);
-    Pending* pend = (Pending*)(G.pending + (int64_t)c.grow * sizeof(Pending));
+    init_ctx(G, row, slice, q, c);
+    const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S);
+    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)c.grow * sizeof(Pending));
     if ((!c.live && !c.want_out) || c.forced) {
         if (slice != 0) return;
         if (threadIdx.x == 0) pend->mode = kPendNone;
         if (!c.forced) {
-            if (threadIdx.x == 0 && G.tokens) G.tokens[row] = kPad;
+            if (threadIdx.x == 0 && gp(G.tokens)) gp(G.tokens)[row] = kPad;
             return;
         }
         if (c.want_out) write_outputs<ES>(G, c, sm, -INFINITY, 0.0f, false);
@@ -2078,7 +2244,7 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
         pub_st_summary(&w.summ[slice], s);
     }
     if (c.S > 1) {
-        if (!arrive_last(G.counters + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
+        if (!arrive_last(gp(G.counters) + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
         if (threadIdx.x == 0) sm.foreign = 0;
@@ -2094,7 +2260,7 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     constexpr int E = 16 / ES;
     constexpr int NCH = kNV / E;
     constexpr int NSB = NCH * kWaves;
-    Pending* pend = (Pending*)(G.pending + (int64_t)(G.row_begin + row) * sizeof(Pending));
+    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)(G.row_begin + row) * sizeof(Pending));
     const Pending P = *pend;
     if (P.mode != kPendNucleus) return;
     const Geo geo = slice_geo_at<ES>(G, row, slice);
@@ -2104,7 +2270,7 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     preload(G, row, geo, PL);
     Ctx c;
     init_ctx(G, row, slice, c);
-    const RowWs w = row_ws(G.ws + (int64_t)row * G.ws_row_bytes, c.S);
+    const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S);
     Tile T;
     finish_tile<ES>(G, c, geo, R, PL, T, sm);
     // everything above the boundary bin survives: its sums per sub-block; the bin's values go to the finaliser
@@ -2125,7 +2291,7 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
         pub_st(&s.hi_mass, hi_mass);
     }
     if (c.S > 1) {
-        if (!arrive_last(G.counters + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
+        if (!arrive_last(gp(G.counters) + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
         if (threadIdx.x == 0) sm.foreign = 0;
@@ -2171,7 +2337,7 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
         exact = idx >= 0 && idx < ntot;
         if (exact) thr = key_float(sm.u.c.key[idx]);
     }
-    const bool need_tok = G.tokens != nullptr || (G.flags & MIS_UPDATE_STATE);
+    const bool need_tok = gp(G.tokens) != nullptr || (G.flags & MIS_UPDATE_STATE);
     const float fe = drop_eos ? eos_value<ES>(G, c, sm) : -INFINITY;
     if (!exact) {
         tok = slow_path<ES>(G, c, sm, m, P.z, drop_eos, thr);
@@ -2211,6 +2377,14 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     finish_row<ES>(G, c, sm, tok, thr, m, drop_eos);
 }
 
+// The kernel arguments, read in place from the kernarg segment (a by-value parameter indexed with a run-time
+// group index can be copied whole to scratch).
+__device__ __forceinline__ const KernelArgs& kernel_args() {
+    return *(const KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+}
+
+
+
 __device__ __forceinline__ bool locate(const KernelArgs& args, int& gi, int& row, int& slice) {
     const int x = blockIdx.x % 8;
     int i = blockIdx.x / 8;
@@ -2228,10 +2402,8 @@ __device__ __forceinline__ bool locate(const KernelArgs& args, int& gi, int& row
 }
 
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_kernel(const KernelArgs args_in) {
-    // the arguments are read in place through the kernarg segment (indexing the by-value parameter with a
-    // run-time group index can make the compiler copy all of it to scratch)
     (void)args_in;
-    const KernelArgs& args = *(const KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    const KernelArgs& args = kernel_args();
     __shared__ Smem sm;
     int gi, row, slice;
     if (!locate(args, gi, row, slice)) return;
@@ -2245,10 +2417,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
 // The nucleus pass over the sample kernel's grid: the workgroups of rows with a pending record redo their slice
 // and resolve the row; every other workgroup leaves after reading that record.
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args_in) {
-    // the arguments are read in place through the kernarg segment (indexing the by-value parameter with a
-    // run-time group index can make the compiler copy all of it to scratch)
     (void)args_in;
-    const KernelArgs& args = *(const KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    const KernelArgs& args = kernel_args();
     __shared__ Smem sm;
     int gi, row, slice;
     if (!locate(args, gi, row, slice)) return;
