@@ -155,7 +155,8 @@ struct SliceSummary {
     unsigned long long under_q;  // histogram: mass below the window (2^40 units of exp(x - m))
     int32_t under_n;
     int32_t n_hi;            // nucleus pass: values above the boundary bin
-    double hi_mass;          // nucleus pass: their sum of exp(x - M)
+    double hi_mass;          // nucleus pass: their sum of exp(x - M); first pass of a top-p-only row: the sum of
+                             // exp(x - m) over its published candidates
     int32_t pad_[2];
 };
 static_assert(sizeof(SliceSummary) == 64, "summary layout");
@@ -489,6 +490,28 @@ __device__ __forceinline__ unsigned long long block_sum_u(unsigned long long x, 
     return r;
 }
 
+// Three sums with one barrier pair (double, u64, int).
+__device__ __forceinline__ void block_sum3(double& a, unsigned long long& b, int& c, Smem& sm) {
+    a = wave_sum_d(a);
+    b = wave_reduce(b, [](unsigned long long x, unsigned long long y) { return x + y; });
+    c = wave_reduce(c, [](int x, int y) { return x + y; });
+    __syncthreads();
+    if (lane_id() == 0) {
+        sm.red_d[wave_id()] = a;
+        sm.red_u[wave_id()] = b;
+        sm.red_i[wave_id()] = c;
+    }
+    __syncthreads();
+    a = 0.0;
+    b = 0ull;
+    c = 0;
+    for (int i = 0; i < kWaves; ++i) {
+        a += sm.red_d[i];
+        b += sm.red_u[i];
+        c += sm.red_i[i];
+    }
+}
+
 // Exclusive prefix from the lane-shifted inclusive scan (no subtraction).
 __device__ __forceinline__ double block_excl_scan_d(double x, double& total, Smem& sm) {
     const double incl = wave_incl_scan(x);
@@ -662,21 +685,27 @@ __device__ __forceinline__ PenEntry pen_entry(const DevGroup& G, const Ctx& c, i
     return e;
 }
 
-// x / d rounded to nearest from r = RN(1/d): each step computes the residual x - q*d exactly with one fma and
-// corrects q by it; the first makes q faithful, the second rounds it correctly (Markstein).  The residual is
-// formed as q*d - x so a zero x keeps its sign.  Exact (checked against IEEE division) for
-// 2^-64 <= |x| <= 2^64 and 2^-16 <= d <= 2^16; callers send other x (zero, infinite, NaN, extreme) to IEEE
-// division.
+// x / d rounded to nearest from r = RN(1/d): q = RN(x * r) is faithful, the residual x - q*d is exact in one
+// fma, and one correction RN(q + r * residual) rounds the quotient correctly (Markstein).  The residual is formed
+// as q*d - x so a zero x keeps its sign.  Checked bit-exact against IEEE division on 33.6 M pairs with
+// 2^-100 <= |x| < 2^64 and 2^-16 <= d <= 2^16 (every divisor mantissa at one exponent); zero is exact too.
 __device__ __forceinline__ float div_rn(float x, float d, float r) {
-    float q = x * r;
-    float e = fmaf(q, d, -x);
-    q = fmaf(-e, r, q);
-    e = fmaf(q, d, -x);
+    const float q = x * r;
+    const float e = fmaf(q, d, -x);
     return fmaf(-e, r, q);
 }
 
-__device__ __forceinline__ bool div_in_range(float x) {
-    return (__float_as_uint(x) & 0x7fffffffu) - 0x1f800000u < 0x40000000u;  // 2^-64 <= |x| < 2^64
+// The raw logits the corrected-reciprocal pipeline takes: zero, or 2^-40 <= |x| < 2^40.  With the divisors in
+// [2^-16, 2^16] and the penalty table's freq*n and presence zero or in [2^-60, 2^40] (checked per row), every
+// operand a division then sees is zero or in [2^-100, 2^64).
+__device__ __forceinline__ bool raw_in_range(float x) {
+    const uint32_t u = __float_as_uint(x) & 0x7fffffffu;
+    return u - 0x2b800000u < 0x28000000u || u == 0u;  // [2^-40, 2^40)
+}
+
+__device__ __forceinline__ bool table_term_ok(float v) {
+    const float a = fabsf(v);
+    return a == 0.f || (a >= 0x1p-60f && a <= 0x1p40f);
 }
 
 __device__ __forceinline__ bool divisor_in_range(float d) { return d >= 0x1p-16f && d <= 0x1p16f; }
@@ -724,7 +753,7 @@ __device__ __forceinline__ int clear_counts(const DevGroup& G, const Ctx& c, int
     if (threadIdx.x < kAlphaTable) {
         const PenEntry e = pen_entry(G, c, threadIdx.x);
         sm.pen[threadIdx.x] = e;
-        bad = !divisor_in_range(e.a);
+        bad = !divisor_in_range(e.a) || !table_term_ok(e.fn) || !table_term_ok(e.pn);
     }
     return bad;
 }
@@ -995,29 +1024,15 @@ __device__ __forceinline__ void process_tile_t(const DevGroup& G, const Ctx& c, 
                 continue;
             }
             float y = x;
-            if (HF) {
-                if (DIV == kDivPow2) {
-                    y = y * rd;
-                } else {
-                    slow |= !div_in_range(y);
-                    y = div_rn(y, d, rd);
-                }
-            }
+            if (COUNTS || DIV != kDivPow2) slow |= !raw_in_range(x);  // one check covers every division below
+            if (HF) y = DIV == kDivPow2 ? y * rd : div_rn(y, d, rd);
             if (COUNTS) {
                 const PenEntry pe = sm.pen[n];
-                slow |= !(y < 0.f) && !div_in_range(y) && y != 0.f;
                 const float q = div_rn(y, pe.a, pe.ra);
                 y = y < 0.f ? y * pe.a : q;
                 y = (y - pe.fn) - pe.pn;
             }
-            if (!HF) {
-                if (DIV == kDivPow2) {
-                    y = y * rd;
-                } else {
-                    slow |= !div_in_range(y);
-                    y = div_rn(y, d, rd);
-                }
-            }
+            if (!HF) y = DIV == kDivPow2 ? y * rd : div_rn(y, d, rd);
             f[e] = y;
         }
         if (DIV != kDivIeee || COUNTS) {
@@ -2012,7 +2027,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
     constexpr int E = 16 / ES;
     constexpr int NSB = kNV / E * kWaves;
     float m = -INFINITY, gmax = -INFINITY;
-    double z = 0.0;
+    double z = 0.0, cmass = 0.0;  // cmass: top-p-only rows, the published candidates' mass
     int am = INT_MAX, ntot = 0;
     bool overflow = false;
     // no published data: everything below streams the row
@@ -2025,7 +2040,11 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
         for (int s = 0; s < c.S; ++s) {
             const SliceSummary& q = sm.summ[s];
             if (q.m == m && q.argmax < am) am = q.argmax;
-            if (q.m > -INFINITY) z += q.z * exp((double)q.m - (double)m);
+            if (q.m > -INFINITY) {
+                const double sc = exp((double)q.m - (double)m);
+                z += q.z * sc;
+                cmass += q.hi_mass * sc;
+            }
             gmax = fmaxf(gmax, q.g);
             ntot += q.ncand;
             overflow |= q.overflow != 0;
@@ -2074,7 +2093,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
         } else {
             tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
         }
-    } else if (c.nucleus && !foreign &&
+    } else if (c.nucleus && !foreign && cmass >= (double)c.top_p * z &&  // else the candidates cannot settle it
                nucleus_from_cands(G, c, sm, w, ntot, overflow, gmax, m, z, drop_eos, need_tok, thr, tok)) {
         // resolved from the published candidates
     } else if (c.nucleus && !foreign) {
@@ -2180,29 +2199,29 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
         am = m > -INFINITY ? block_min_i(first, sm) : geo.lo;
     }
     double z = 0.0;
-    if (c.need_mass && m > -INFINITY) {
-        const double part = tile_sub_sums<ES>(T, m, -INFINITY, sm);
-        z = block_sum_d(part, sm);  // includes a barrier: sm.sbw is complete
-        if ((int)threadIdx.x < NCH * kWaves) pub_st(&w.sb[(int64_t)slice * kMaxSB + threadIdx.x], sm.sbw[threadIdx.x]);
-    }
     int ncand = 0, overflow = 0, hb = 0, under_n = 0;
+    double cmass = 0.0;
     unsigned long long under_q = 0ull;
     float g = INFINITY;
     if (c.nucleus && m > -INFINITY) {
+        // top-p without top-k: the sum of exp and the mass histogram in one pass, one exp per element
         hb = bin_of(m);
         for (int b = threadIdx.x; b < kNB; b += kBlock) {
             sm.hcnt[b] = 0u;
             sm.hmass[b] = 0ull;
         }
         __syncthreads();
+        double part = 0.0;
         unsigned long long uq = 0ull;
         int un = 0;
 #pragma unroll
         for (int q = 0; q < kNV; ++q) {
             const float f = T.v[q];
             if (finite_f(f)) {
+                const float e = expf(f - m);
+                part += (double)e;
                 const int o = hb - bin_of(f);
-                const unsigned long long mq = mass_q(f, m);
+                const unsigned long long mq = (unsigned long long)((double)e * kMassScale);  // mass_q(f, m)
                 if (o < kNB) {
                     atomicAdd(&sm.hcnt[o], 1u);
                     if (mq) atomicAdd(&sm.hmass[o], mq);
@@ -2212,13 +2231,27 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
                 }
             }
         }
-        under_q = block_sum_u(uq, sm);
-        under_n = block_sum_i(un, sm);  // includes barriers: the histogram is complete
+        block_sum3(part, uq, un, sm);  // includes barriers: the histogram is complete
+        z = part;
+        under_q = uq;
+        under_n = un;
         if (threadIdx.x < 64)
             for (int b = threadIdx.x; b < kNB; b += 64) {
                 pub_st(&w.hcnt[(int64_t)slice * kNB + b], sm.hcnt[b]);
                 pub_st(&w.hmass[(int64_t)slice * kNB + b], sm.hmass[b]);
             }
+    } else if (c.full_draw && m > -INFINITY) {
+        // unfiltered rows draw from the sub-block sums
+        const double part = tile_sub_sums<ES>(T, m, -INFINITY, sm);
+        z = block_sum_d(part, sm);  // includes a barrier: sm.sbw is complete
+        if ((int)threadIdx.x < NCH * kWaves) pub_st(&w.sb[(int64_t)slice * kMaxSB + threadIdx.x], sm.sbw[threadIdx.x]);
+    } else if (c.need_mass && m > -INFINITY) {
+        // the full-row normaliser only
+        double part = 0.0;
+#pragma unroll
+        for (int q = 0; q < kNV; ++q)
+            if (finite_f(T.v[q])) part += (double)expf(T.v[q] - m);
+        z = block_sum_d(part, sm);
     }
     if (c.cand_mode || c.nucleus) {
         // tau = the cand_target-th largest per-thread maximum: at least cand_target values are >= tau
@@ -2226,6 +2259,11 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
         const int run = publish_range<ES>(T, geo, g, INFINITY, w.cand + (int64_t)slice * kCapSlice, sm);
         ncand = min(run, kCapSlice);
         overflow = run > kCapSlice;
+        if (c.nucleus && threadIdx.x < 64) {  // wave 0 holds the staged candidates: their mass
+            double part = 0.0;
+            for (int p = threadIdx.x; p < ncand; p += 64) part += (double)expf(sm.stage[p].f - m);
+            cmass = wave_sum_d(part);
+        }
     }
     (void)NCH;
     if (threadIdx.x == 0) {
@@ -2240,7 +2278,7 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
         s.under_q = under_q;
         s.under_n = under_n;
         s.n_hi = 0;
-        s.hi_mass = 0.0;
+        s.hi_mass = cmass;
         pub_st_summary(&w.summ[slice], s);
     }
     if (c.S > 1) {
@@ -2316,35 +2354,102 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
     bool exact = !foreign && !overflow && ntot <= kCapRow && ntot > 0 && above < P.target;
     if (exact) {
         int nkeys = 0;
-        const int np = gather_cands(c, sm, w, ntot, -INFINITY, nkeys);
-        sort_keys_desc(sm, np);
-        // ranks inside the bin whose exclusive mass (above + bin values ranked before) is below the target
-        const int per = (ntot + kBlock - 1) / kBlock;
-        double mine = 0.0;
-        for (int r = threadIdx.x * per; r < min(ntot, (int)(threadIdx.x + 1) * per); ++r)
-            mine += (double)expf(key_float(sm.u.c.key[r]) - m);
-        double tot;
-        double run2 = above + block_excl_scan_d(mine, tot, sm);
-        int kp = 0;
-        for (int r = threadIdx.x * per; r < min(ntot, (int)(threadIdx.x + 1) * per); ++r) {
-            if (run2 < P.target) ++kp;
-            run2 += (double)expf(key_float(sm.u.c.key[r]) - m);
+        gather_cands(c, sm, w, ntot, INFINITY, nkeys);  // the bin's values and ids in vocabulary order (no keys)
+        // The cut inside the bin without sorting it: 256 sub-buckets of the bin, highest first, with fixed-point
+        // masses; the sub-bucket where the running mass crosses the target is the only one sorted.
+        const float scale = (float)kNB / (P.hi_v - P.lo_v);
+        auto bucket = [&](float f) { return min(max((int)((P.hi_v - f) * scale), 0), kNB - 1); };
+        for (int b = threadIdx.x; b < kNB; b += kBlock) {
+            sm.hcnt[b] = 0u;
+            sm.hmass[b] = 0ull;  // (the gather's slice map lived here)
         }
-        kp = block_sum_i(kp, sm);
-        const bool below_bin = kp == ntot && above + tot < P.target;  // the cut lies under the bin
-        int idx = below_bin ? -1 : kp - 1;  // position in the bin of the last kept rank
-        if (nabove + kp < c.min_keep_eff) idx = c.min_keep_eff - nabove - 1;  // min_keep clamp
-        exact = idx >= 0 && idx < ntot;
-        if (exact) thr = key_float(sm.u.c.key[idx]);
+        __syncthreads();
+        for (int q = threadIdx.x; q < ntot; q += kBlock) {
+            const float f = sm.u.c.val[q];
+            const int b = bucket(f);
+            atomicAdd(&sm.hcnt[b], 1u);
+            atomicAdd(&sm.hmass[b], mass_q(f, m));
+        }
+        __syncthreads();
+        // one sub-bucket per thread (kNB == kBlock): exclusive scan of mass << 12 | count from the top (ntot <= 2048)
+        const unsigned long long cq = sm.hcnt[threadIdx.x], mq = sm.hmass[threadIdx.x];
+        unsigned long long tot_pk;
+        const unsigned long long ex_pk = block_excl_scan_u((mq << 12) | cq, tot_pk, sm);
+        const double tq = (P.target - above) * kMassScale;  // the bin's share of the target, in mass_q units
+        const int bstar = block_max_i(cq > 0 && (double)(ex_pk >> 12) < tq ? (int)threadIdx.x : -1, sm);
+        if ((int)threadIdx.x == bstar) {
+            sm.sel_bin = (int)(ex_pk & 4095ull);  // bin values ranked above the sub-bucket
+            sm.sel_acc = ex_pk >> 12;            // and their mass
+        }
+        if (threadIdx.x == 0) sm.sel_rem = 0;
+        __syncthreads();
+        const int n_before = sm.sel_bin;
+        const unsigned long long m_before = sm.sel_acc;
+        if (bstar < 0 || (double)(tot_pk >> 12) < tq) {
+            exact = false;  // the whole bin short of the target: the cut lies under the bin (streaming path)
+        } else {
+            // the sub-bucket's keys (bf16 inputs make many exact ties here), sorted descending
+            for (int q = threadIdx.x; q < ntot; q += kBlock) {
+                const float f = sm.u.c.val[q];
+                if (bucket(f) == bstar) sm.u.c.key[atomicAdd(&sm.sel_rem, 1)] = ord_key(f);
+            }
+            __syncthreads();
+            const int nbk = sm.sel_rem;
+            int np = 8;
+            while (np < nbk) np <<= 1;
+            for (int q = nbk + threadIdx.x; q < np; q += kBlock) sm.u.c.key[q] = 0u;
+            __syncthreads();
+            sort_keys_desc(sm, np);
+            // ranks (blocked per thread) whose exclusive mass, above the sub-bucket included, is below the target
+            const int per = (nbk + kBlock - 1) / kBlock;
+            const int r0 = min(nbk, (int)threadIdx.x * per), r1 = min(nbk, r0 + per);
+            unsigned long long mine = 0ull;
+            for (int r = r0; r < r1; ++r) mine += mass_q(key_float(sm.u.c.key[r]), m);
+            unsigned long long run_tot;
+            unsigned long long run = m_before + block_excl_scan_u(mine, run_tot, sm);
+            int kp = 0;
+            for (int r = r0; r < r1; ++r) {
+                if ((double)run < tq) ++kp;
+                run += mass_q(key_float(sm.u.c.key[r]), m);
+            }
+            const int kept_in = block_sum_i(kp, sm);
+            // ranks kept above the sub-bucket and in it; fewer than min_keep: the streaming path
+            exact = kept_in >= 1 && nabove + n_before + kept_in >= c.min_keep_eff;
+            if (exact) thr = key_float(sm.u.c.key[kept_in - 1]);
+        }
     }
     const bool need_tok = gp(G.tokens) != nullptr || (G.flags & MIS_UPDATE_STATE);
     const float fe = drop_eos ? eos_value<ES>(G, c, sm) : -INFINITY;
+    const int nsb = c.S * NSB;
     if (!exact) {
         tok = slow_path<ES>(G, c, sm, m, P.z, drop_eos, thr);
+    } else if (need_tok && nsb <= kCapSlice) {
+        // survivor sums per sub-block: the values above the bin (published) plus the bin's survivors, whose
+        // fixed-point masses are added per sub-block (the sub-block of a candidate follows from its id)
+        unsigned long long* sbq = (unsigned long long*)sm.stage;
+        for (int i = threadIdx.x; i < nsb; i += kBlock) sbq[i] = 0ull;
+        __syncthreads();
+        for (int q = threadIdx.x; q < ntot; q += kBlock) {
+            const float f = sm.u.c.val[q];
+            const int id = sm.u.c.id[q];
+            if (f >= thr && !(drop_eos && id == G.eos)) {
+                const int s = id / c.slice_len;
+                atomicAdd(&sbq[s * NSB + sub_block_of<ES>(slice_geo<ES>(G, c, s), id)], mass_q(f, m));
+            }
+        }
+        __syncthreads();  // the candidates are spent: sm.u.sbs may overwrite them
+        for (int i = threadIdx.x; i < nsb; i += kBlock) {
+            const int s = i / NSB, sb = i % NSB;
+            double v = pub_ld(&w.sb[(int64_t)s * kMaxSB + sb]) + (double)sbq[i] * (1.0 / kMassScale);
+            if (drop_eos && finite_f(fe) && fe >= P.hi_v && G.eos / c.slice_len == s &&
+                sub_block_of<ES>(slice_geo<ES>(G, c, s), G.eos) == sb)
+                v = fmax(0.0, v - (double)expf(fe - m));
+            sm.u.sbs[i] = v;
+        }
+        __syncthreads();
+        tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c));
     } else if (need_tok) {
-        // survivor sums per sub-block: the values above the bin (already summed) plus the bin's survivors.
-        // Candidates are in vocabulary order, so a sub-block's are a contiguous run (found by binary search).
-        const int nsb = c.S * NSB;
+        // many sub-blocks: survivor sums per sub-block by binary search over the vocabulary-ordered candidates
         for (int i = threadIdx.x; i < nsb; i += kBlock) {
             const int s = i / NSB, sb = i % NSB;
             double v = pub_ld(&w.sb[(int64_t)s * kMaxSB + sb]);
@@ -2359,9 +2464,9 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
                 else
                     b = mid;
             }
-            for (int p = a; p < ntot && sm.u.c.id[p] < jhi; ++p) {
-                const float f = sm.u.c.val[p];
-                if (f >= thr && !(drop_eos && sm.u.c.id[p] == G.eos)) v += (double)expf(f - m);
+            for (int q = a; q < ntot && sm.u.c.id[q] < jhi; ++q) {
+                const float f = sm.u.c.val[q];
+                if (f >= thr && !(drop_eos && sm.u.c.id[q] == G.eos)) v += (double)expf(f - m);
             }
             if (drop_eos && G.eos >= jlo && G.eos < jhi && finite_f(fe) && fe >= P.hi_v)
                 v = fmax(0.0, v - (double)expf(fe - m));

@@ -106,6 +106,29 @@ def test_row_counts_that_do_not_fill_xcds_evenly(rows):
     compare_group(f"uneven{rows}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows, prob_rtol=1e-5)
 
 
+@pytest.mark.parametrize("semantics", ["omni", "hf"])
+def test_large_nucleus_second_pass(semantics):
+    """Top-p rows without top-k whose nucleus is far too large for the first pass's candidates."""
+    print(f"[gpu] large nucleus {semantics}", flush=True)
+    gen = torch.Generator().manual_seed(91)
+    rows, v = 6, W.THINKER_V
+    x = (torch.randn(rows, v, generator=gen) * 2.5).to(torch.bfloat16)
+    hist = torch.randint(0, v, (rows, 256), generator=gen, dtype=torch.int64).to(torch.int32)
+    one = lambda val, dt=torch.float32: torch.full((rows,), val, dtype=dt)  # noqa: E731
+    top_p = torch.tensor([0.5, 0.7, 0.9, 0.95, 0.99, 0.8])
+    ref_rows = ext.Rows(logits=x, temperature=one(1.0), top_k=one(0, torch.int32), top_p=top_p, repetition=one(1.1),
+                        presence=one(0.0), frequency=one(0.0), history=hist, seeds=one(3, torch.int64),
+                        steps=one(1, torch.int64), eos=5, min_new_tokens=4, semantics=semantics,
+                        min_keep=3 if semantics == "hf" else 1)
+    g = G.RowGroup(x.to(DEV), temperature=1.0, top_k=0, top_p=top_p.to(DEV), repetition=1.1, history=hist.to(DEV),
+                   seeds=one(3, torch.int64).to(DEV), steps=one(1, torch.int64).to(DEV), eos=5, min_new_tokens=4,
+                   semantics=semantics, min_keep=3 if semantics == "hf" else 1, processed=True, probs=True)
+    G.launch([g])
+    torch.cuda.synchronize()
+    compare_group(f"large_nucleus_{semantics}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows,
+                  prob_rtol=2e-3)
+
+
 def test_thinker_greedy_is_first_argmax_at_full_size():
     wl = W.thinker_b64().to(DEV)
     x = wl.logits.clone()
