@@ -25,18 +25,22 @@
 //          candidates in vocabulary order;
 //        unfiltered rows: walks the sub-block sums to the sub-block holding
 //          u * total and rescans only that sub-block;
-//        larger nuclei: merges the histograms, finds the bin that holds the
-//          top-p boundary and leaves a pending record;
+//        larger nuclei: merges the histograms and finds the bin that holds
+//          the top-p boundary (see below);
 //        anything the fast paths cannot prove exactly, or a row whose slices
 //          ran on more than one XCD: streams the row again and selects by radix
 //          over order-preserving keys.
-// nucleus_kernel (the same grid; workgroups of rows without a pending record
-// leave at once) re-reads only the slices of pending rows, publishes the values
-// inside the boundary bin and the sums of everything above it, and its last
-// workgroup per row resolves the top-p threshold exactly and draws.
-// Workgroups never wait for one another: the only cross-workgroup protocol is
-// publish / arrive / read on the per-row arrival word, which the finaliser
-// resets for the next launch.
+//   5. a top-p row without top-k holds its other slices after they arrive: each
+//      waits on the row's decision word, which the finaliser sets once it knows
+//      whether the boundary bin is needed.  If it is, every slice (the finaliser
+//      after re-reading its own) publishes from its registers the values inside
+//      the bin and the sums of everything above it, and the last to arrive again
+//      resolves the top-p threshold exactly and draws.  A waiting slice only ever
+//      waits for the finaliser, which arrived last and is already running, so the
+//      wait ends however the workgroups are scheduled.
+// Apart from that wait, the only cross-workgroup protocol is publish / arrive /
+// read on the per-row arrival word, which the finaliser resets for the next
+// launch.
 
 #include <hip/hip_runtime.h>
 
@@ -68,12 +72,15 @@ constexpr int kAlphaTable = 64;      // rep**n for n < 64 kept in LDS (larger co
 constexpr float kBinScale = 8.0f;    // bins of 1/8 logit
 constexpr int kMaxRows = 16384;      // rows per launch
 constexpr int kCounterStride = 32;  // u32 words between rows' counters: one 128-byte line each (no atomic contention)
+constexpr int kDecisionWord = 2;    // in a row's counter line, after the 64-bit arrival word
 constexpr int64_t kCounterBytes = 4 * kCounterStride * (int64_t)kMaxRows;
 constexpr int64_t kPendingBytes = 64 * (int64_t)kMaxRows;
 constexpr int64_t kPad = -1;
 constexpr double kMassScale = 1099511627776.0;  // 2^40 fixed-point units of exp(x - max)
 
-enum : int32_t { kPendNone = 0, kPendNucleus = 1 };
+// The finaliser's decision for the held slices of a top-p row without top-k (0: not yet decided).
+enum : uint32_t { kHeldDone = 1, kHeldBin = 2 };
+constexpr int kSpinLimit = 1 << 22;  // bound on a held slice's wait (each try sleeps ~64 clocks): ~0.2 s
 
 struct DevGroup {
     const char* logits;
@@ -162,7 +169,7 @@ struct SliceSummary {
 static_assert(sizeof(SliceSummary) == 64, "summary layout");
 
 struct Pending {
-    int32_t mode;
+    int32_t mode_;
     float lo_v, hi_v;        // boundary bin [lo_v, hi_v)
     float m;                 // row max
     double z;                // full-row sum of exp(x - m)
@@ -241,7 +248,8 @@ struct Smem {
     int32_t sel_rem;
     int32_t is_last;
     int32_t foreign;  // the row's slices ran on more than one XCD: their publications are not readable here
-    int32_t pad_;
+    uint32_t decision;  // held slices: the finaliser's decision (kHeld*), 0 before it is made
+    Pending held;       // held slices: the boundary bin
     unsigned long long sel_acc;
     float sel_tau;
 };
@@ -909,7 +917,7 @@ struct Preload {
     bool hvec;
 };
 
-__device__ __forceinline__ void preload(const DevGroup& G, int row, const Geo& g, Preload& P) {
+__device__ __forceinline__ void preload(const DevGroup& G, int row, const Geo& g, Preload& P, bool history = true) {
     const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)row * G.allowed_stride : nullptr;
     const int wb = g.first >> 5;  // arithmetic shift: first may be negative in slice 0
     const int wmax = (G.vocab - 1) >> 5;
@@ -923,7 +931,7 @@ __device__ __forceinline__ void preload(const DevGroup& G, int row, const Geo& g
         P.mw[u] = m;
     }
     const char* hrow = gp(G.history) != nullptr && G.hist_len > 0 ? hist_row(G, row) : nullptr;
-    P.hvec = hrow != nullptr && hist_vec(G, hrow);
+    P.hvec = history && hrow != nullptr && hist_vec(G, hrow);
     if (P.hvec) {
         const int4* h4 = (const int4*)hrow;
         const int nv = G.hist_len >> 2;
@@ -1600,6 +1608,55 @@ __device__ __forceinline__ bool arrive_last(unsigned int* counter, int S, Smem& 
     return sm.is_last != 0;
 }
 
+// Held slices.  The slices of a top-p row without top-k (and S > 1) that are not last to arrive wait for the
+// finaliser's decision word, kept next to the arrival word.  The finaliser is the row's last arrival, so it is
+// running by the time anyone waits, and it sets the word on every path; the wait is bounded all the same.
+__device__ __forceinline__ bool holds_slices(const Ctx& c) { return c.nucleus && c.S > 1; }
+
+__device__ __forceinline__ unsigned int* row_counter(const DevGroup& G, const Ctx& c) {
+    return gp(G.counters) + (int64_t)c.grow * kCounterStride;
+}
+
+// The finaliser's side (thread 0; the first call wins).  Stores issued before it (the pending record, the
+// arrival word's reset) complete before the decision is visible.
+__device__ __forceinline__ void release_held(const DevGroup& G, const Ctx& c, Smem& sm, uint32_t d) {
+    if (!holds_slices(c) || threadIdx.x != 0 || sm.decision != 0u) return;
+    sm.decision = d;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __hip_atomic_store(row_counter(G, c) + kDecisionWord, d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A held slice's side: the decision (0 if the bound ran out, which leaves the slice without a part to play).
+__device__ __forceinline__ uint32_t await_decision(const DevGroup& G, const Ctx& c, Smem& sm) {
+    if (threadIdx.x == 0) {
+        unsigned int* word = row_counter(G, c) + kDecisionWord;
+        uint32_t d = 0u;
+        for (int i = 0; i < kSpinLimit; ++i) {
+            d = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d != 0u) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        sm.decision = d;
+    }
+    __syncthreads();
+    return sm.decision;
+}
+
+// A held slice that is not needed counts itself out on the arrival word (which the finaliser reset); the last of
+// the S - 1 clears the arrival and decision words for the next launch.
+__device__ __forceinline__ void depart(const DevGroup& G, const Ctx& c) {
+    if (threadIdx.x != 0) return;
+    unsigned long long* word = (unsigned long long*)row_counter(G, c);
+    const unsigned long long old =
+        __hip_atomic_fetch_add(word, 1ull << (7 * xcc_id()), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int total = 1;
+    for (int f = 0; f < 8; ++f) total += (int)((old >> (7 * f)) & 127ull);
+    if (total == c.S - 1) {
+        __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(row_counter(G, c) + kDecisionWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // ---------------------------------------------------------------- finaliser pieces
 
 // One bitonic compare-exchange step on 8 keys per lane (key index i = 8 * t + r): the lower index of each pair
@@ -1978,6 +2035,7 @@ __device__ __forceinline__ bool nucleus_from_cands(const DevGroup& G, const Ctx&
     // target, would need values that were not published
     const bool settled = gmax == -INFINITY || kept < nge || (kept == nge && zge >= (double)c.top_p * z);
     if (!settled) return false;
+    release_held(G, c, sm, kHeldDone);
     thr = t;
     if (need_tok) tok = cand_draw(G, c, sm, ntot, thr, m, drop_eos, row_uniform(G, c));
     return true;
@@ -2022,8 +2080,10 @@ __device__ __forceinline__ void stream_stats(const DevGroup& G, const Ctx& c, Sm
     z = block_sum_d(zpart, sm);
 }
 
+// Returns true when the row's boundary bin is needed: the pending record is stored and the held slices released
+// to publish it; the caller then resolves its own slice's part.
 template <int ES>
-__device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
+__device__ __forceinline__ bool finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
     constexpr int E = 16 / ES;
     constexpr int NSB = kNV / E * kWaves;
     float m = -INFINITY, gmax = -INFINITY;
@@ -2032,7 +2092,9 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
     bool overflow = false;
     // no published data: everything below streams the row
     const bool foreign = sm.foreign != 0 || (G.flags & MIS_FINALIZE_STREAMING) != 0;
+    if (threadIdx.x == 0) sm.decision = 0u;
     if (foreign) {
+        release_held(G, c, sm, kHeldDone);  // the held slices' publications would not be readable here
         stream_stats<ES>(G, c, sm, m, am, z);
     } else {
         load_summaries<ES>(c, sm, w);
@@ -2136,7 +2198,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
         if (bstar >= 0 && bstar < kNB - 1 && !below_window) {
             if (threadIdx.x == 0) {
                 Pending p;
-                p.mode = kPendNucleus;
+                p.mode_ = 0;
                 p.lo_v = (float)(HB - bstar) / kBinScale;
                 p.hi_v = (float)(HB - bstar + 1) / kBinScale;
                 p.m = m;
@@ -2144,47 +2206,29 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Ctx& c, Smem& 
                 p.target = target;
                 *pend = p;
             }
-            return;  // the nucleus pass draws and updates the state
+            release_held(G, c, sm, kHeldBin);
+            return true;  // the row's slices resolve the bin, and the last of them draws
         }
+        release_held(G, c, sm, kHeldDone);
         tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
     } else {
+        release_held(G, c, sm, kHeldDone);
         tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
     }
-    if (threadIdx.x == 0) pend->mode = kPendNone;
+    release_held(G, c, sm, kHeldDone);
     finish_row<ES>(G, c, sm, tok, thr, m, drop_eos);
+    return false;
 }
 
 // ---------------------------------------------------------------- the slice phase
 
+// The slice phase's results: max, first argmax (greedy rows), normaliser and, by row kind, the mass histogram,
+// sub-block sums or candidates, then the slice's summary.
 template <int ES>
-__device__ __forceinline__ void run_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
+__device__ __forceinline__ void publish_slice(const DevGroup& G, const Ctx& c, const Geo& geo, const Tile& T,
+                                              const RowWs& w, const int slice, Smem& sm) {
     constexpr int E = 16 / ES;
     constexpr int NCH = kNV / E;
-    // the row's parameters, then the slice's tile, mask words and history go out before any of them is used
-    RowParams q;
-    load_params(G, row, q);
-    const Geo geo = slice_geo_at<ES>(G, row, slice);
-    RawTile<ES> R;
-    issue_tile<ES>(geo, R);
-    Preload P;
-    preload(G, row, geo, P);
-    Ctx c;
-    init_ctx(G, row, slice, q, c);
-    const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S);
-    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)c.grow * sizeof(Pending));
-    if ((!c.live && !c.want_out) || c.forced) {
-        if (slice != 0) return;
-        if (threadIdx.x == 0) pend->mode = kPendNone;
-        if (!c.forced) {
-            if (threadIdx.x == 0 && gp(G.tokens)) gp(G.tokens)[row] = kPad;
-            return;
-        }
-        if (c.want_out) write_outputs<ES>(G, c, sm, -INFINITY, 0.0f, false);
-        update_state(G, c, G.eos);
-        return;
-    }
-    Tile T;
-    finish_tile<ES>(G, c, geo, R, P, T, sm);
     float tm = -INFINITY;
 #pragma unroll
     for (int q = 0; q < kNV; ++q) tm = fmaxf(tm, T.v[q]);
@@ -2265,7 +2309,6 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
             cmass = wave_sum_d(part);
         }
     }
-    (void)NCH;
     if (threadIdx.x == 0) {
         SliceSummary s;
         s.m = m;
@@ -2281,36 +2324,86 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
         s.hi_mass = cmass;
         pub_st_summary(&w.summ[slice], s);
     }
-    if (c.S > 1) {
-        if (!arrive_last(gp(G.counters) + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
-    } else {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
-        if (threadIdx.x == 0) sm.foreign = 0;
-        __syncthreads();
-    }
-    finalize<ES>(G, c, sm, w);
 }
 
-// ---------------------------------------------------------------- the nucleus pass
+template <int ES>
+__device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, const Geo& geo, const Tile& T,
+                                            const RowWs& w, const int slice, Smem& sm);
 
 template <int ES>
-__device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
-    constexpr int E = 16 / ES;
-    constexpr int NCH = kNV / E;
-    constexpr int NSB = NCH * kWaves;
-    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)(G.row_begin + row) * sizeof(Pending));
-    const Pending P = *pend;
-    if (P.mode != kPendNucleus) return;
+__device__ __forceinline__ void run_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
+    // the row's parameters, then the slice's tile, mask words and history go out before any of them is used
+    RowParams q;
+    load_params(G, row, q);
     const Geo geo = slice_geo_at<ES>(G, row, slice);
     RawTile<ES> R;
     issue_tile<ES>(geo, R);
-    Preload PL;
-    preload(G, row, geo, PL);
+    Preload P;
+    preload(G, row, geo, P);
     Ctx c;
-    init_ctx(G, row, slice, c);
+    init_ctx(G, row, slice, q, c);
     const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S);
+    if ((!c.live && !c.want_out) || c.forced) {
+        if (slice != 0) return;
+        if (!c.forced) {
+            if (threadIdx.x == 0 && gp(G.tokens)) gp(G.tokens)[row] = kPad;
+            return;
+        }
+        if (c.want_out) write_outputs<ES>(G, c, sm, -INFINITY, 0.0f, false);
+        update_state(G, c, G.eos);
+        return;
+    }
     Tile T;
-    finish_tile<ES>(G, c, geo, R, PL, T, sm);
+    finish_tile<ES>(G, c, geo, R, P, T, sm);
+    publish_slice<ES>(G, c, geo, T, w, slice, sm);
+    // the branches below are uniform: read through readfirstlane so the compiler keeps them as scalar branches
+    // (a branch it takes for divergent would run both sides and keep T live across the finaliser)
+    bool held = false;
+    if (c.S > 1 && !uni((int)arrive_last(row_counter(G, c), c.S, sm))) {
+        if (!holds_slices(c)) return;
+        const uint32_t d = (uint32_t)uni((int)await_decision(G, c, sm));
+        if (d == kHeldDone) depart(G, c);
+        if (d != kHeldBin) return;
+        held = true;  // this slice's values are still in T
+    } else {
+        if (c.S == 1) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
+            if (threadIdx.x == 0) sm.foreign = 0;
+            __syncthreads();
+        }
+        if (!uni((int)finalize<ES>(G, c, sm, w))) return;
+    }
+    if (!held) {  // the finaliser's registers did not keep its slice: the slice again
+        issue_tile<ES>(geo, R);
+        preload(G, row, geo, P, false);  // (the counts then load the history themselves)
+        finish_tile<ES>(G, c, geo, R, P, T, sm);
+    }
+    resolve_bin<ES>(G, c, geo, T, w, slice, sm);
+}
+
+// ---------------------------------------------------------------- the boundary bin
+
+// A held slice's part once the row needs its boundary bin [lo_v, hi_v) (the pending record): the sums per
+// sub-block of its values above the bin and the values inside it, published; the last of the row's slices to
+// arrive then finds the exact top-p threshold inside the bin and draws.
+template <int ES>
+__device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, const Geo& geo, const Tile& T,
+                                            const RowWs& w, const int slice, Smem& sm) {
+    constexpr int E = 16 / ES;
+    constexpr int NCH = kNV / E;
+    constexpr int NSB = NCH * kWaves;
+    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)c.grow * sizeof(Pending));
+    if (threadIdx.x == 0) {
+        Pending p;
+        p.lo_v = pub_ld(&pend->lo_v);
+        p.hi_v = pub_ld(&pend->hi_v);
+        p.m = pub_ld(&pend->m);
+        p.z = pub_ld(&pend->z);
+        p.target = pub_ld(&pend->target);
+        sm.held = p;
+    }
+    __syncthreads();
+    const Pending P = sm.held;
     // everything above the boundary bin survives: its sums per sub-block; the bin's values go to the finaliser
     const double part = tile_sub_sums<ES>(T, P.m, P.hi_v, sm);
     int nhi = 0;
@@ -2329,7 +2422,10 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
         pub_st(&s.hi_mass, hi_mass);
     }
     if (c.S > 1) {
-        if (!arrive_last(gp(G.counters) + (int64_t)c.grow * kCounterStride, c.S, sm)) return;
+        if (!arrive_last(row_counter(G, c), c.S, sm)) return;
+        // every held slice has read the decision word: clear it for the next launch
+        if (threadIdx.x == 0)
+            __hip_atomic_store(row_counter(G, c) + kDecisionWord, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
         if (threadIdx.x == 0) sm.foreign = 0;
@@ -2478,7 +2574,6 @@ __device__ __forceinline__ void nucleus_row(const DevGroup& G, const int row, co
         __syncthreads();
         tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c));
     }
-    if (threadIdx.x == 0) pend->mode = kPendNone;
     finish_row<ES>(G, c, sm, tok, thr, m, drop_eos);
 }
 
@@ -2519,21 +2614,6 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) 
         run_row<4>(G, row, slice, sm);
 }
 
-// The nucleus pass over the sample kernel's grid: the workgroups of rows with a pending record redo their slice
-// and resolve the row; every other workgroup leaves after reading that record.
-__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4, 8))) void nucleus_kernel(const KernelArgs args_in) {
-    (void)args_in;
-    const KernelArgs& args = kernel_args();
-    __shared__ Smem sm;
-    int gi, row, slice;
-    if (!locate(args, gi, row, slice)) return;
-    const DevGroup& G = args.g[gi];
-    if (G.es == 2)
-        nucleus_row<2>(G, row, slice, sm);
-    else
-        nucleus_row<4>(G, row, slice, sm);
-}
-
 __global__ void uniform_kernel(const int64_t* seeds, const int64_t* steps, const int64_t* rids, int64_t n, int rng,
                                float* out) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -2561,16 +2641,6 @@ int max_slice_elems(int es) { return kBlock * kNV - 16 / es; }
 
 // Workspace: [arrival counters, kCounterBytes][pending records, kPendingBytes][per group: rows x row regions].
 constexpr int64_t kFixedBytes = kCounterBytes + kPendingBytes;
-
-// Whether some row of the group can be a top-p-only row (no top-k), which needs the nucleus pass.
-bool may_need_nucleus(const MisGroup& g) {
-    const bool k_all = g.top_k != nullptr ||
-                       ((g.flags & MIS_TOPK_ZERO_DISABLES) && g.top_k_value <= 0) ||
-                       std::max(g.top_k_value, g.min_keep) >= g.vocab;
-    const bool p_on = g.top_p != nullptr || !((g.flags & MIS_TOPP_ONE_DISABLES) && g.top_p_value >= 1.0f);
-    const bool sampling = g.temperature != nullptr || g.temperature_value > 0.0f;
-    return k_all && p_on && sampling;
-}
 
 int check_group(const MisGroup& g, int idx) {
     if (!g.logits && g.rows > 0) return fail(MIS_E_ARG, "group %d: logits is NULL", idx);
@@ -2634,7 +2704,6 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     memset(&a, 0, sizeof a);
     a.n_groups = n_groups;
     int blocks = 0, rows_total = 0;
-    bool nucleus = false;
     size_t ws_off = (size_t)kFixedBytes;
     for (int i = 0; i < n_groups; ++i) {
         const MisGroup& g = groups[i];
@@ -2697,7 +2766,6 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
         d.counters = (unsigned int*)workspace;
         d.pending = (char*)workspace + kCounterBytes;
         d.gi = i;
-        nucleus |= g.rows > 0 && may_need_nucleus(g);
         ws_off += (size_t)d.ws_row_bytes * (size_t)g.rows;
         const int64_t nb = (int64_t)g.rows * d.slices;
         if (nb + blocks > (int64_t)1 << 30) return fail(MIS_E_UNSUPPORTED, "too many rows");
@@ -2722,13 +2790,8 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     a.per_xcd = (int)*std::max_element(count, count + 8);
     const int grid = a.per_xcd * 8;
     hipLaunchKernelGGL(sample_kernel, dim3(grid), dim3(kBlock), 0, (hipStream_t)stream, a);
-    hipError_t e = hipGetLastError();
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
-    if (nucleus) {
-        hipLaunchKernelGGL(nucleus_kernel, dim3(grid), dim3(kBlock), 0, (hipStream_t)stream, a);
-        e = hipGetLastError();
-        if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
-    }
     return 0;
 }
 

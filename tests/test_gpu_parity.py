@@ -129,6 +129,37 @@ def test_large_nucleus_second_pass(semantics):
                   prob_rtol=2e-3)
 
 
+def test_boundary_bin_and_candidate_rows_across_launches():
+    """Launches on one workspace that alternate between top-p rows needing their boundary bin (wide nuclei) and
+    rows the first pass's candidates settle (sharp rows): the arrival and decision words must start every launch
+    cleared, whichever way the previous launch released its held slices."""
+    print("[gpu] boundary bin across launches", flush=True)
+    gen = torch.Generator().manual_seed(23)
+    rows, v = 5, W.THINKER_V
+    wide = (torch.randn(rows, v, generator=gen) * 2.5).to(torch.bfloat16)
+    sharp = (torch.randn(rows, v, generator=gen) * 9.0).to(torch.bfloat16)
+    hist = torch.randint(0, v, (rows, 128), generator=gen, dtype=torch.int64).to(torch.int32)
+    one = lambda val, dt=torch.float32: torch.full((rows,), val, dtype=dt)  # noqa: E731
+    x_dev, p_dev = wide.to(DEV), one(0.9).to(DEV)
+    steps_dev = one(1, torch.int64).to(DEV)
+    g = G.RowGroup(x_dev, temperature=1.0, top_k=0, top_p=p_dev, repetition=1.05, history=hist.to(DEV),
+                   seeds=torch.arange(rows, dtype=torch.int64).to(DEV), steps=steps_dev, eos=5, min_new_tokens=2,
+                   semantics="hf", min_keep=3, processed=True, probs=True)
+    plan = [(wide, 0.95), (sharp, 0.5), (wide, 0.9), (wide, 0.99), (sharp, 0.8), (wide, 0.7)]
+    for it, (x, tp) in enumerate(plan):
+        x_dev.copy_(x.to(DEV))
+        p_dev.fill_(tp)
+        steps_dev.fill_(it + 1)
+        G.launch([g])
+        torch.cuda.synchronize()
+        ref_rows = ext.Rows(logits=x, temperature=one(1.0), top_k=one(0, torch.int32), top_p=one(tp),
+                            repetition=one(1.05), presence=one(0.0), frequency=one(0.0), history=hist,
+                            seeds=torch.arange(rows, dtype=torch.int64), steps=one(it + 1, torch.int64), eos=5,
+                            min_new_tokens=2, semantics="hf", min_keep=3)
+        compare_group(f"across_launches_{it}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows,
+                      prob_rtol=2e-3)
+
+
 def test_thinker_greedy_is_first_argmax_at_full_size():
     wl = W.thinker_b64().to(DEV)
     x = wl.logits.clone()
