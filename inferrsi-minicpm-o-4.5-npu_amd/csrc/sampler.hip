@@ -240,7 +240,12 @@ struct Smem {
     unsigned long long red_u[kWaves];
     float red_f[kWaves];
     int32_t red_i[kWaves];
-    double tile_sum[kMaxSlices];
+    double tile_sum[kMaxSlices];  // streaming draw: slice sums; finaliser: per-slice scale exp(m_s - m)
+    struct {
+        double z, cmass;
+        float m, gmax;
+        int32_t am, ntot, overflow;
+    } fin;  // the finaliser's merge of the slice summaries
     SliceSummary summ[kMaxSlices];
     Cand stage[kCapSlice];  // a slice's published candidates, copied out by wave 0
     int32_t coff[kMaxSlices + 1];  // finaliser: candidate offsets per slice
@@ -342,12 +347,18 @@ __device__ __forceinline__ int fresh_tid() {
 __device__ __forceinline__ int fresh_lane() { return fresh_tid() & 63; }
 
 // Cross-lane moves.  Each computes its own lane arithmetic, so no lane index is shared (and kept live) across the
-// kernel: xor offsets below 32 use ds_swizzle's bit-mask mode (the pattern is an immediate), the others
-// ds_bpermute.
+// kernel: xor offsets 1, 2 and 8 are DPP moves, 4 and 16 ds_swizzle's bit-mask mode (the pattern is an
+// immediate), the others ds_bpermute.
 template <int O>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t x) {
     static_assert(O >= 1 && O <= 32 && (O & (O - 1)) == 0, "power-of-two offset");
-    if constexpr (O == 32)
+    if constexpr (O == 1)
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    else if constexpr (O == 2)
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else if constexpr (O == 8)
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);  // row_ror:8 = lane ^ 8
+    else if constexpr (O == 32)
         return (uint32_t)__builtin_amdgcn_ds_bpermute((fresh_lane() ^ 32) << 2, (int)x);
     else
         return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1f | (O << 10));  // lane ^ O within 32 lanes
@@ -1575,6 +1586,19 @@ __device__ __forceinline__ float block_kth_of_256(float v, int c, Smem& sm) {
     return sm.sel_tau;
 }
 
+// Appends key to sm.u.c.key at sm.sel_rem where pred holds (any order): one LDS atomic per wave, positions
+// within the wave from the ballot.
+__device__ __forceinline__ void append_key(bool pred, uint32_t key, Smem& sm) {
+    const unsigned long long b = __ballot(pred);
+    if (b == 0ull) return;
+    const int leader = __ffsll((long long)b) - 1;
+    int base = 0;
+    if (lane_id() == leader) base = atomicAdd(&sm.sel_rem, __popcll(b));
+    base = __builtin_amdgcn_readlane(base, leader);
+    const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    if (pred) sm.u.c.key[base + below] = key;
+}
+
 // ---------------------------------------------------------------- cross-workgroup protocol
 
 __device__ __forceinline__ unsigned xcc_id() {
@@ -1659,81 +1683,97 @@ __device__ __forceinline__ void depart(const DevGroup& G, const Ctx& c) {
 
 // ---------------------------------------------------------------- finaliser pieces
 
-// One bitonic compare-exchange step on 8 keys per lane (key index i = 8 * t + r): the lower index of each pair
-// keeps the larger key where the k-block sorts descending.
-template <int J>
-__device__ __forceinline__ void bitonic_lane_step(uint32_t (&a)[8], int t, int k) {
-    const bool desc_lane = ((8 * t) & k) == 0;  // the direction of every pair of the lane once k >= 8
+// One compare-exchange step (block size K, partner distance J) of a descending bitonic sort over R keys per lane,
+// element i = R * gl + r (gl: the lane's index among the sorting lanes).  Partners within a lane are in registers,
+// within a wave across lanes, across waves through LDS.
+template <int R, int K, int J>
+__device__ __forceinline__ void bitonic_step(uint32_t (&a)[R], int gl, Smem& sm) {
+    if constexpr (J < R) {
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        if (r & J) continue;
-        const bool desc = k >= 8 ? desc_lane : ((8 * t + r) & k) == 0;
-        const uint32_t lo = min(a[r], a[r | J]), hi = max(a[r], a[r | J]);
-        a[r] = desc ? hi : lo;
-        a[r | J] = desc ? lo : hi;
+        for (int r = 0; r < R; ++r) {
+            if (r & J) continue;
+            bool desc;
+            if constexpr (K >= R)
+                desc = ((R * gl) & K) == 0;
+            else
+                desc = (r & K) == 0;
+            const uint32_t lo = min(a[r], a[r | J]), hi = max(a[r], a[r | J]);
+            a[r] = desc ? hi : lo;
+            a[r | J] = desc ? lo : hi;
+        }
+    } else {
+        constexpr int D = J / R;  // lane distance
+        const bool keep_max = (((R * gl) & J) == 0) == (((R * gl) & K) == 0);  // lower of the pair in a desc block
+        if constexpr (D < 64) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t b = xor_lane<D>(a[r]);
+                a[r] = keep_max ? max(a[r], b) : min(a[r], b);
+            }
+        } else {
+            __syncthreads();  // every wave sorts when partners cross waves
+#pragma unroll
+            for (int r = 0; r < R; ++r) sm.u.c.key[R * gl + r] = a[r];
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t b = sm.u.c.key[(R * gl + r) ^ J];
+                a[r] = keep_max ? max(a[r], b) : min(a[r], b);
+            }
+        }
     }
 }
 
-// Sorts sm.u.c.key[0, np) descending (np a power of two in [8, kCapRow]; the keys past the candidates are zero,
-// below every real key).  Up to kBlock keys: rank sort.  Beyond: bitonic network over 8 keys per lane, partners
-// within a lane in registers, within a wave by shuffles, across waves through LDS (strides >= 512); up to 512 keys
-// are sorted by wave 0 alone.
-__device__ __forceinline__ void sort_keys_desc(Smem& sm, int np) {
-    if (np <= kBlock) {
-        // rank sort: thread t counts the keys ahead of key t (larger, or equal at a lower position)
-        const int t = threadIdx.x;
-        const uint32_t mine = t < np ? sm.u.c.key[t] : 0u;
-        int rank = 0;
-        if (t < np) {
-#pragma unroll 2
-            for (int q = 0; q < np; q += 8) {  // np >= 8 is a power of two
-                const uint4 o0 = *(const uint4*)&sm.u.c.key[q];
-                const uint4 o1 = *(const uint4*)&sm.u.c.key[q + 4];
-                const uint32_t o[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+template <int R, int K, int J>
+__device__ __forceinline__ void bitonic_merge(uint32_t (&a)[R], int gl, Smem& sm) {
+    bitonic_step<R, K, J>(a, gl, sm);
+    if constexpr (J > 1) bitonic_merge<R, K, J / 2>(a, gl, sm);
+}
+
+template <int N, int R, int K>
+__device__ __forceinline__ void bitonic_stages(uint32_t (&a)[R], int gl, Smem& sm) {
+    bitonic_merge<R, K, K / 2>(a, gl, sm);
+    if constexpr (K < N) bitonic_stages<N, R, K * 2>(a, gl, sm);
+}
+
+// N keys (a power of two, 64..kCapRow) sorted descending in place: wave 0 alone up to 128 keys (no barrier),
+// every wave beyond.  Fully unrolled.
+template <int N>
+__device__ __forceinline__ void sort_n(Smem& sm) {
+    constexpr int NW = N <= 128 ? 1 : kWaves;
+    constexpr int R = N / (64 * NW);
+    static_assert(R >= 1 && R <= 8 && R * 64 * NW == N, "keys per lane");
+    if (NW == kWaves || wave_id() == 0) {
+        const int gl = fresh_tid();
+        uint32_t a[R];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) rank += (o[e] > mine || (o[e] == mine && q + e < t)) ? 1 : 0;
-            }
-        }
-        __syncthreads();
-        if (t < np) sm.u.c.key[rank] = mine;
-        __syncthreads();
-        return;
-    }
-    const int nw = np <= 512 ? 1 : kWaves;
-    const int N = 512 * nw;
-    if (wave_id() < nw) {
-        const int t = threadIdx.x;
-        uint32_t a[8];
+        for (int r = 0; r < R; ++r) a[r] = sm.u.c.key[R * gl + r];
+        bitonic_stages<N, R, 2>(a, gl, sm);
+        if constexpr (NW > 1) __syncthreads();  // the last cross-wave reads are done
 #pragma unroll
-        for (int r = 0; r < 8; ++r) a[r] = 8 * t + r < np ? sm.u.c.key[8 * t + r] : 0u;
-        for (int k = 2; k <= N; k <<= 1) {
-            for (int j = k >> 1; j >= 8; j >>= 1) {
-                uint32_t b[8];
-                if (j >= 512) {
-                    __syncthreads();  // every wave is here: nw == kWaves
-#pragma unroll
-                    for (int r = 0; r < 8; ++r) sm.u.c.key[8 * t + r] = a[r];
-                    __syncthreads();
-#pragma unroll
-                    for (int r = 0; r < 8; ++r) b[r] = sm.u.c.key[(8 * t + r) ^ j];
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 8; ++r) b[r] = shfl_xor_d(a[r], j >> 3);
-                }
-                // j >= 8 and k > j: both bits come from the lane, not from r
-                const bool keep_max = (((8 * t) & j) == 0) == (((8 * t) & k) == 0);
-#pragma unroll
-                for (int r = 0; r < 8; ++r) a[r] = keep_max ? max(a[r], b[r]) : min(a[r], b[r]);
-            }
-            if (k >= 8) bitonic_lane_step<4>(a, t, k);
-            if (k >= 4) bitonic_lane_step<2>(a, t, k);
-            bitonic_lane_step<1>(a, t, k);
-        }
-        if (nw == kWaves) __syncthreads();  // the last cross-wave reads are done
-#pragma unroll
-        for (int r = 0; r < 8; ++r) sm.u.c.key[8 * t + r] = a[r];
+        for (int r = 0; r < R; ++r) sm.u.c.key[R * gl + r] = a[r];
     }
     __syncthreads();
+}
+
+// Sorts sm.u.c.key[0, np) descending (np a power of two in [8, kCapRow]; the keys past the candidates are zero,
+// below every real key).
+__device__ __forceinline__ void sort_keys_desc(Smem& sm, int np) {
+    if (np < 64) {
+        for (int p = np + (int)threadIdx.x; p < 64; p += kBlock) sm.u.c.key[p] = 0u;
+        __syncthreads();
+    }
+    switch (np) {
+        case 8:
+        case 16:
+        case 32:
+        case 64: sort_n<64>(sm); break;
+        case 128: sort_n<128>(sm); break;
+        case 256: sort_n<256>(sm); break;
+        case 512: sort_n<512>(sm); break;
+        case 1024: sort_n<1024>(sm); break;
+        default: sort_n<2048>(sm); break;
+    }
 }
 
 // The top-k / top-p threshold from the sorted candidate keys (vocabulary counts n >= ...).  z_full is the
@@ -1903,6 +1943,41 @@ __device__ __forceinline__ void load_summaries(const Ctx& c, Smem& sm, const Row
     __syncthreads();
 }
 
+// The row's max, first argmax, normaliser, published-candidate count and gate from the slice summaries, one lane
+// of wave 0 per slice; each slice's scale exp(m_s - m) stays in sm.tile_sum (0 for a slice with no finite value).
+__device__ __forceinline__ void merge_summaries(const Ctx& c, Smem& sm, const RowWs& w) {
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const bool v = l < c.S;
+        SliceSummary q;
+        if (v) {
+            q = pub_ld_summary(&w.summ[l]);
+            sm.summ[l] = q;
+        }
+        const float qm = v ? q.m : -INFINITY;
+        const float m = wave_reduce(qm, [](float a, float b) { return fmaxf(a, b); });
+        const int am = wave_reduce(v && qm == m ? q.argmax : INT_MAX, [](int a, int b) { return min(a, b); });
+        const bool fin = v && qm > -INFINITY;
+        const double sc = fin ? exp((double)qm - (double)m) : 0.0;
+        const double z = wave_sum_d(fin ? q.z * sc : 0.0);
+        const double cmass = wave_sum_d(fin ? q.hi_mass * sc : 0.0);
+        const float gmax = wave_reduce(v ? q.g : -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+        const int ntot = wave_reduce(v ? q.ncand : 0, [](int a, int b) { return a + b; });
+        const int ovf = wave_reduce(v ? q.overflow : 0, [](int a, int b) { return a | b; });
+        sm.tile_sum[l] = sc;
+        if (l == 0) {
+            sm.fin.z = z;
+            sm.fin.cmass = cmass;
+            sm.fin.m = m;
+            sm.fin.gmax = gmax;
+            sm.fin.am = am;
+            sm.fin.ntot = ntot;
+            sm.fin.overflow = ovf;
+        }
+    }
+    __syncthreads();
+}
+
 // The slow, always-exact path: stream the row for every selection.
 // The slices' published candidates into LDS in vocabulary order (slice s's at offset coff[s]) and the order keys
 // of those >= gate, packed in no particular order (nkeys of them) and padded with zeros up to np, the returned
@@ -1946,8 +2021,8 @@ __device__ __forceinline__ int gather_cands(const Ctx& c, Smem& sm, const RowWs&
         if (idx < ntot) {
             sm.u.c.val[idx] = cd[u].f;
             sm.u.c.id[idx] = cd[u].j;
-            if (cd[u].f >= gate) sm.u.c.key[atomicAdd(&sm.sel_rem, 1)] = ord_key(cd[u].f);
         }
+        append_key(idx < ntot && cd[u].f >= gate, ord_key(cd[u].f), sm);
     }
     __syncthreads();
     nkeys = sm.sel_rem;
@@ -2080,10 +2155,80 @@ __device__ __forceinline__ void stream_stats(const DevGroup& G, const Ctx& c, Sm
     z = block_sum_d(zpart, sm);
 }
 
+// A top-p row without top-k whose nucleus the published candidates do not settle: the slices' mass histograms,
+// merged on the global 1/8-logit grid below the row's top bin, locate the bin holding the top-p boundary.  When
+// one does, its pending record is stored, the held slices are released to resolve it, and true is returned.
+__device__ __forceinline__ bool pick_bin(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w, float m, double z) {
+    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)c.grow * sizeof(Pending));
+    const int HB = bin_of(m);
+    double gm = 0.0;
+    uint32_t gc = 0u;
+    const int o = threadIdx.x;  // one global bin per thread (kNB == kBlock)
+    for (int s0 = 0; s0 < c.S; s0 += 8) {  // 8 slices' loads in flight at a time
+        unsigned long long hm[8];
+        uint32_t hc[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int s = s0 + u;
+            hm[u] = 0ull;
+            hc[u] = 0u;
+            if (s < c.S && sm.summ[s].m > -INFINITY) {
+                const int os = o - (HB - sm.summ[s].hb);
+                if (os >= 0 && os < kNB) {
+                    hm[u] = pub_ld(&w.hmass[(int64_t)s * kNB + os]);
+                    hc[u] = pub_ld(&w.hcnt[(int64_t)s * kNB + os]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int s = s0 + u;
+            if (hc[u] != 0u || hm[u] != 0ull)
+                gm += (double)hm[u] * (1.0 / kMassScale) * sm.tile_sum[s];
+            gc += hc[u];
+        }
+    }
+    double ztot;
+    const double before = block_excl_scan_d(gm, ztot, sm);
+    const double target = (double)c.top_p * z;
+    const int bstar = block_max_i((gc > 0u && before < target) ? o : -1, sm);
+    int under = 0;
+    for (int s = 0; s < c.S; ++s) under += sm.summ[s].under_n;
+    const bool below_window = ztot < target && under > 0;  // the boundary may lie under the window
+    if (bstar >= 0 && bstar < kNB - 1 && !below_window) {
+        if (threadIdx.x == 0) {
+            Pending p;
+            p.mode_ = 0;
+            p.lo_v = (float)(HB - bstar) / kBinScale;
+            p.hi_v = (float)(HB - bstar + 1) / kBinScale;
+            p.m = m;
+            p.z = z;
+            p.target = target;
+            *pend = p;
+        }
+        release_held(G, c, sm, kHeldBin);
+        return true;
+    }
+    return false;
+}
+
+// The finaliser of a top-p row without top-k, before anything else: when the published candidates cannot hold
+// the nucleus (their mass is short of top_p), the boundary bin is chosen at once, while the finaliser's slice is
+// still in registers.  Merges the summaries (the finaliser is then told so).
+__device__ __forceinline__ bool early_bin(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
+    if (sm.foreign != 0 || (G.flags & MIS_FINALIZE_STREAMING) != 0) return false;
+    merge_summaries(c, sm, w);
+    const float m = sm.fin.m;
+    const double z = sm.fin.z;
+    if (!(m > -INFINITY) || sm.fin.cmass >= (double)c.top_p * z) return false;
+    if (threadIdx.x == 0) sm.decision = 0u;
+    return pick_bin(G, c, sm, w, m, z);
+}
+
 // Returns true when the row's boundary bin is needed: the pending record is stored and the held slices released
 // to publish it; the caller then resolves its own slice's part.
 template <int ES>
-__device__ __forceinline__ bool finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w) {
+__device__ __forceinline__ bool finalize(const DevGroup& G, const Ctx& c, Smem& sm, const RowWs& w, bool merged) {
     constexpr int E = 16 / ES;
     constexpr int NSB = kNV / E * kWaves;
     float m = -INFINITY, gmax = -INFINITY;
@@ -2097,22 +2242,15 @@ __device__ __forceinline__ bool finalize(const DevGroup& G, const Ctx& c, Smem& 
         release_held(G, c, sm, kHeldDone);  // the held slices' publications would not be readable here
         stream_stats<ES>(G, c, sm, m, am, z);
     } else {
-        load_summaries<ES>(c, sm, w);
-        for (int s = 0; s < c.S; ++s) m = fmaxf(m, sm.summ[s].m);
-        for (int s = 0; s < c.S; ++s) {
-            const SliceSummary& q = sm.summ[s];
-            if (q.m == m && q.argmax < am) am = q.argmax;
-            if (q.m > -INFINITY) {
-                const double sc = exp((double)q.m - (double)m);
-                z += q.z * sc;
-                cmass += q.hi_mass * sc;
-            }
-            gmax = fmaxf(gmax, q.g);
-            ntot += q.ncand;
-            overflow |= q.overflow != 0;
-        }
+        if (!merged) merge_summaries(c, sm, w);
+        m = sm.fin.m;
+        am = sm.fin.am;
+        z = sm.fin.z;
+        cmass = sm.fin.cmass;
+        gmax = sm.fin.gmax;
+        ntot = sm.fin.ntot;
+        overflow = sm.fin.overflow != 0;
     }
-    Pending* pend = (Pending*)(gp(G.pending) + (int64_t)c.grow * sizeof(Pending));
     const bool drop_eos = c.hf && c.censor;
     const bool need_tok = gp(G.tokens) != nullptr || (G.flags & MIS_UPDATE_STATE);
     int64_t tok = kPad;
@@ -2127,8 +2265,7 @@ __device__ __forceinline__ bool finalize(const DevGroup& G, const Ctx& c, Smem& 
             const int nsb = c.S * NSB;
             for (int i = threadIdx.x; i < nsb; i += kBlock) {
                 const int s = i / NSB;
-                const double sc = sm.summ[s].m > -INFINITY ? exp((double)sm.summ[s].m - (double)m) : 0.0;
-                sm.u.sbs[i] = pub_ld(&w.sb[(int64_t)s * kMaxSB + (i % NSB)]) * sc;
+                sm.u.sbs[i] = pub_ld(&w.sb[(int64_t)s * kMaxSB + (i % NSB)]) * sm.tile_sum[s];
             }
             __syncthreads();
             if (drop_eos) {
@@ -2159,56 +2296,7 @@ __device__ __forceinline__ bool finalize(const DevGroup& G, const Ctx& c, Smem& 
                nucleus_from_cands(G, c, sm, w, ntot, overflow, gmax, m, z, drop_eos, need_tok, thr, tok)) {
         // resolved from the published candidates
     } else if (c.nucleus && !foreign) {
-        // merge the slices' mass histograms on the global 1/8-logit grid, below the row's top bin
-        const int HB = bin_of(m);
-        double gm = 0.0;
-        uint32_t gc = 0u;
-        const int o = threadIdx.x;  // one global bin per thread (kNB == kBlock)
-        for (int s0 = 0; s0 < c.S; s0 += 8) {  // 8 slices' loads in flight at a time
-            unsigned long long hm[8];
-            uint32_t hc[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int s = s0 + u;
-                hm[u] = 0ull;
-                hc[u] = 0u;
-                if (s < c.S && sm.summ[s].m > -INFINITY) {
-                    const int os = o - (HB - sm.summ[s].hb);
-                    if (os >= 0 && os < kNB) {
-                        hm[u] = pub_ld(&w.hmass[(int64_t)s * kNB + os]);
-                        hc[u] = pub_ld(&w.hcnt[(int64_t)s * kNB + os]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int s = s0 + u;
-                if (hc[u] != 0u || hm[u] != 0ull)
-                    gm += (double)hm[u] * (1.0 / kMassScale) * exp((double)sm.summ[s].m - (double)m);
-                gc += hc[u];
-            }
-        }
-        double ztot;
-        const double before = block_excl_scan_d(gm, ztot, sm);
-        const double target = (double)c.top_p * z;
-        const int bstar = block_max_i((gc > 0u && before < target) ? o : -1, sm);
-        int under = 0;
-        for (int s = 0; s < c.S; ++s) under += sm.summ[s].under_n;
-        const bool below_window = ztot < target && under > 0;  // the boundary may lie under the window
-        if (bstar >= 0 && bstar < kNB - 1 && !below_window) {
-            if (threadIdx.x == 0) {
-                Pending p;
-                p.mode_ = 0;
-                p.lo_v = (float)(HB - bstar) / kBinScale;
-                p.hi_v = (float)(HB - bstar + 1) / kBinScale;
-                p.m = m;
-                p.z = z;
-                p.target = target;
-                *pend = p;
-            }
-            release_held(G, c, sm, kHeldBin);
-            return true;  // the row's slices resolve the bin, and the last of them draws
-        }
+        if (pick_bin(G, c, sm, w, m, z)) return true;  // the row's slices resolve the bin, the last of them draws
         release_held(G, c, sm, kHeldDone);
         tok = slow_path<ES>(G, c, sm, m, z, drop_eos, thr);
     } else {
@@ -2358,25 +2446,26 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
     publish_slice<ES>(G, c, geo, T, w, slice, sm);
     // the branches below are uniform: read through readfirstlane so the compiler keeps them as scalar branches
     // (a branch it takes for divergent would run both sides and keep T live across the finaliser)
-    bool held = false;
     if (c.S > 1 && !uni((int)arrive_last(row_counter(G, c), c.S, sm))) {
         if (!holds_slices(c)) return;
         const uint32_t d = (uint32_t)uni((int)await_decision(G, c, sm));
         if (d == kHeldDone) depart(G, c);
         if (d != kHeldBin) return;
-        held = true;  // this slice's values are still in T
+        // this slice's values are still in T
     } else {
         if (c.S == 1) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the slice's publications are in the L2
             if (threadIdx.x == 0) sm.foreign = 0;
             __syncthreads();
         }
-        if (!uni((int)finalize<ES>(G, c, sm, w))) return;
-    }
-    if (!held) {  // the finaliser's registers did not keep its slice: the slice again
-        issue_tile<ES>(geo, R);
-        preload(G, row, geo, P, false);  // (the counts then load the history themselves)
-        finish_tile<ES>(G, c, geo, R, P, T, sm);
+        const bool merged = c.nucleus;
+        if (!(c.nucleus && uni((int)early_bin(G, c, sm, w)))) {
+            if (!uni((int)finalize<ES>(G, c, sm, w, merged))) return;
+            // the bin after the candidates failed: the finaliser's registers did not keep its slice
+            issue_tile<ES>(geo, R);
+            preload(G, row, geo, P, false);  // (the counts then load the history themselves)
+            finish_tile<ES>(G, c, geo, R, P, T, sm);
+        }
     }
     resolve_bin<ES>(G, c, geo, T, w, slice, sm);
 }
@@ -2485,9 +2574,10 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
             exact = false;  // the whole bin short of the target: the cut lies under the bin (streaming path)
         } else {
             // the sub-bucket's keys (bf16 inputs make many exact ties here), sorted descending
-            for (int q = threadIdx.x; q < ntot; q += kBlock) {
-                const float f = sm.u.c.val[q];
-                if (bucket(f) == bstar) sm.u.c.key[atomicAdd(&sm.sel_rem, 1)] = ord_key(f);
+            for (int q0 = 0; q0 < ntot; q0 += kBlock) {  // block-uniform trip count (append_key ballots)
+                const int q = q0 + threadIdx.x;
+                const float f = q < ntot ? sm.u.c.val[q] : -INFINITY;
+                append_key(q < ntot && bucket(f) == bstar, ord_key(f), sm);
             }
             __syncthreads();
             const int nbk = sm.sel_rem;
