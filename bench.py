@@ -11,8 +11,8 @@ enough copies of the logits that no copy is still cached (the 256 MB
 last-level cache) when it is read again, and are replayed from a HIP graph so
 the host never throttles the queue.  Prints one JSON line on stdout.
 
-A step is the sample kernel plus, when a row of the batch has top-p without
-top-k and a nucleus too large for the first pass, the nucleus kernel; the
+A step is one launch of the sample kernel (rows whose top-p nucleus is too
+large for the published candidates resolve their boundary bin inside it); the
 roofline figure divides the step's algorithmic bytes by the step time.  Its
 ``traffic`` (HBM bytes per step) comes from the rocprof FETCH_SIZE and
 WRITE_SIZE counters recorded in profiles/traffic_thinker_b64.json, each scaled
