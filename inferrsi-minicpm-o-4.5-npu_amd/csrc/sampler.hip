@@ -130,7 +130,7 @@ struct DevGroup {
     unsigned int* counters;  // arrival counters (fixed workspace prefix, zero between launches)
     char* pending;           // per-row pending records (fixed workspace region)
     int32_t gi;              // index of this group in the launch
-    int32_t pad2_;
+    int32_t tiles;           // rows can be top-p without top-k: their row regions hold the processed-tile area
     int64_t ws_row_bytes;
 };
 
@@ -183,27 +183,32 @@ struct Cand {
     int32_t j;
 };
 
-// Row workspace: [S summaries][S x kMaxSB sub-block sums][S x kNB bin counts][S x kNB bin masses][S x kCapSlice cands]
+// Row workspace: [S summaries][S x kMaxSB sub-block sums][S x kNB bin counts][S x kNB bin masses]
+// [S x kCapSlice cands] and, for groups that can have top-p rows without top-k, [S x kNV x kBlock processed values]
+// (a slice's tile as its threads hold it, slot-major: the boundary-bin draw reads one sub-block of it).
 struct RowWs {
     SliceSummary* summ;
     double* sb;
     uint32_t* hcnt;
     unsigned long long* hmass;
     Cand* cand;
+    float* tile;  // null without the tile area
 };
 
-__host__ __device__ __forceinline__ int64_t row_ws_bytes(int s) {
-    const int64_t b = (int64_t)s * (sizeof(SliceSummary) + 8 * kMaxSB + 12 * kNB + sizeof(Cand) * kCapSlice);
+__host__ __device__ __forceinline__ int64_t row_ws_bytes(int s, bool tiles) {
+    int64_t b = (int64_t)s * (sizeof(SliceSummary) + 8 * kMaxSB + 12 * kNB + sizeof(Cand) * kCapSlice);
+    if (tiles) b += (int64_t)s * kNV * kBlock * 4;
     return (b + 255) & ~(int64_t)255;
 }
 
-__device__ __forceinline__ RowWs row_ws(char* base, int s) {
+__device__ __forceinline__ RowWs row_ws(char* base, int s, bool tiles) {
     RowWs w;
     w.summ = (SliceSummary*)base;
     w.sb = (double*)(base + (int64_t)s * sizeof(SliceSummary));
     w.hcnt = (uint32_t*)((char*)w.sb + (int64_t)s * 8 * kMaxSB);
     w.hmass = (unsigned long long*)((char*)w.hcnt + (int64_t)s * 4 * kNB);
     w.cand = (Cand*)((char*)w.hmass + (int64_t)s * 8 * kNB);
+    w.tile = tiles ? (float*)((char*)w.cand + (int64_t)s * sizeof(Cand) * kCapSlice) : nullptr;
     return w;
 }
 
@@ -1837,10 +1842,11 @@ __device__ __forceinline__ int cand_draw(const DevGroup& G, const Ctx& c, Smem& 
 
 // Inverse-CDF draw from sub-block sums: sums[sbi] (already in units of exp(x - m), survivors only, flattened
 // slice-major in vocabulary order) locate the sub-block holding u * total; that sub-block is rescanned element
-// by element (survivors: finite values >= thr, minus EOS when drop_eos).
+// by element (survivors: finite values >= thr, minus EOS when drop_eos), from the published processed tiles when
+// tile is given, else from the logits.
 template <int ES>
 __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, Smem& sm, int nsb_total, float thr,
-                                              float m, bool drop_eos, float u) {
+                                              float m, bool drop_eos, float u, const float* tile = nullptr) {
     constexpr int E = 16 / ES;
     constexpr int NSB = kNV / E * kWaves;
     double zpart = 0.0;
@@ -1877,7 +1883,8 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
     for (int sbi = (first == INT_MAX ? nsb_total : first); sbi < nsb_total; ++sbi) {
         const int s = sbi / NSB, sb = sbi % NSB;
         const Geo g = slice_geo<ES>(G, c, s);
-        if (c.counts && s != cur_slice) build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
+        if (tile == nullptr && c.counts && s != cur_slice)
+            build_counts(G, c, g.first, g.lo, g.hi, (g.hi - g.first + 1) >> 1, sm);
         cur_slice = s;
         // 64 chunks: round sb / kWaves, wave sb % kWaves; wave 0 rescans them
         int found = INT_MAX;
@@ -1892,7 +1899,19 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
                 pv[e] = 0.0f;
                 jv[e] = 0;
             }
-            if (ch < g.nchunk) {
+            if (tile != nullptr) {
+                // slot (round, e) of thread (wave, lane): the tile's layout; out-of-slice slots hold -inf
+                const float* tp = tile + ((int64_t)s * kNV + (sb / kWaves) * E) * kBlock + (sb % kWaves) * 64 +
+                                  (int)threadIdx.x;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const int j = g.first + ch * E + e;
+                    jv[e] = j;
+                    const float f = pub_ld(&tp[e * kBlock]);
+                    if (finite_f(f) && f >= thr && !(drop_eos && j == G.eos)) pv[e] = expf(f - m) * inv;
+                    mine2 += (double)pv[e];
+                }
+            } else if (ch < g.nchunk) {
                 const uint4 raw = *(const uint4*)(g.base + (uintptr_t)ch * 16);
                 const MaskPair mk = mrow ? mask_pair(mrow, nwords, g.first + ch * E) : MaskPair{~0u, ~0u, 0};
 #pragma unroll
@@ -2430,7 +2449,7 @@ __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const 
     preload(G, row, geo, P);
     Ctx c;
     init_ctx(G, row, slice, q, c);
-    const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S);
+    const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S, G.tiles != 0);
     if ((!c.live && !c.want_out) || c.forced) {
         if (slice != 0) return;
         if (!c.forced) {
@@ -2502,6 +2521,11 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
     const double hi_mass = block_sum_d(part, sm);
     nhi = block_sum_i(nhi, sm);
     if ((int)threadIdx.x < NSB) pub_st(&w.sb[(int64_t)slice * kMaxSB + threadIdx.x], sm.sbw[threadIdx.x]);
+    if (w.tile != nullptr) {  // the processed values, for the draw inside one sub-block
+        float* tl = w.tile + (int64_t)slice * kNV * kBlock + threadIdx.x;
+#pragma unroll
+        for (int q = 0; q < kNV; ++q) pub_st(&tl[q * kBlock], T.v[q]);
+    }
     const int run = publish_range<ES>(T, geo, P.lo_v, P.hi_v, w.cand + (int64_t)slice * kCapSlice, sm);
     if (threadIdx.x == 0) {
         SliceSummary& s = w.summ[slice];
@@ -2633,7 +2657,7 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
             sm.u.sbs[i] = v;
         }
         __syncthreads();
-        tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c));
+        tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c), w.tile);
     } else if (need_tok) {
         // many sub-blocks: survivor sums per sub-block by binary search over the vocabulary-ordered candidates
         for (int i = threadIdx.x; i < nsb; i += kBlock) {
@@ -2662,7 +2686,7 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
         __syncthreads();
         for (int i = threadIdx.x; i < nsb; i += kBlock) sm.u.sbs[i] = pub_ld(&w.sb[(int64_t)(i / NSB) * kMaxSB + i % NSB]);
         __syncthreads();
-        tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c));
+        tok = sub_block_draw<ES>(G, c, sm, nsb, thr, m, drop_eos, row_uniform(G, c), w.tile);
     }
     finish_row<ES>(G, c, sm, tok, thr, m, drop_eos);
 }
@@ -2732,6 +2756,15 @@ int max_slice_elems(int es) { return kBlock * kNV - 16 / es; }
 // Workspace: [arrival counters, kCounterBytes][pending records, kPendingBytes][per group: rows x row regions].
 constexpr int64_t kFixedBytes = kCounterBytes + kPendingBytes;
 
+// Whether some row of the group can be a top-p row without top-k (its row regions then hold the tile area).
+bool may_hold_nucleus(const MisGroup& g) {
+    const bool k_all = g.top_k != nullptr || ((g.flags & MIS_TOPK_ZERO_DISABLES) && g.top_k_value <= 0) ||
+                       std::max(g.top_k_value, g.min_keep) >= g.vocab;
+    const bool p_on = g.top_p != nullptr || !((g.flags & MIS_TOPP_ONE_DISABLES) && g.top_p_value >= 1.0f);
+    const bool sampling = g.temperature != nullptr || g.temperature_value > 0.0f;
+    return k_all && p_on && sampling;
+}
+
 int check_group(const MisGroup& g, int idx) {
     if (!g.logits && g.rows > 0) return fail(MIS_E_ARG, "group %d: logits is NULL", idx);
     if (g.dtype != MIS_F32 && g.dtype != MIS_BF16) return fail(MIS_E_ARG, "group %d: unknown dtype %d", idx, g.dtype);
@@ -2781,7 +2814,7 @@ size_t mis_workspace_bytes(const MisGroup* groups, int n_groups) {
         if (check_group(groups[i], i)) return 0;
         const int es = groups[i].dtype == MIS_BF16 ? 2 : 4;
         const int s = (groups[i].vocab + max_slice_elems(es) - 1) / max_slice_elems(es);
-        total += (size_t)row_ws_bytes(s) * (size_t)groups[i].rows;
+        total += (size_t)row_ws_bytes(s, may_hold_nucleus(groups[i])) * (size_t)groups[i].rows;
     }
     return total;
 }
@@ -2851,7 +2884,8 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
         d.row_begin = rows_total;
         rows_total += g.rows;
         if (rows_total > kMaxRows) return fail(MIS_E_UNSUPPORTED, "more than %d rows in one launch", kMaxRows);
-        d.ws_row_bytes = row_ws_bytes(d.slices);
+        d.tiles = may_hold_nucleus(g) ? 1 : 0;
+        d.ws_row_bytes = row_ws_bytes(d.slices, d.tiles != 0);
         d.ws = (char*)workspace + ws_off;
         d.counters = (unsigned int*)workspace;
         d.pending = (char*)workspace + kCounterBytes;
