@@ -259,6 +259,7 @@ struct Smem {
     int32_t is_last;
     int32_t foreign;  // the row's slices ran on more than one XCD: their publications are not readable here
     uint32_t decision;  // held slices: the finaliser's decision (kHeld*), 0 before it is made
+    uint32_t kmin, kmax;  // boundary bin: the extreme keys of the sub-bucket holding the cut
     Pending held;       // held slices: the boundary bin
     unsigned long long sel_acc;
     float sel_tau;
@@ -1849,34 +1850,49 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
                                               float m, bool drop_eos, float u, const float* tile = nullptr) {
     constexpr int E = 16 / ES;
     constexpr int NSB = kNV / E * kWaves;
-    double zpart = 0.0;
-    for (int i = threadIdx.x; i < nsb_total; i += kBlock) zpart += sm.u.sbs[i];
-    const double zs = block_sum_d(zpart, sm);
-    const float inv = 1.0f / (float)zs;
-    const int per = (nsb_total + kBlock - 1) / kBlock;
-    const int lo = min(nsb_total, (int)threadIdx.x * per), hi = min(nsb_total, (int)(threadIdx.x + 1) * per);
-    double mine = 0.0;
-    for (int i = lo; i < hi; ++i) mine += sm.u.sbs[i] * (double)inv;
-    double total;
-    double run = block_excl_scan_d(mine, total, sm);
-    const float target = u * (float)total;
-    int first = INT_MAX;
-    for (int i = lo; i < hi; ++i) {
-        const double nxt = run + sm.u.sbs[i] * (double)inv;
-        if ((float)nxt > target) {
-            first = i;
-            break;
+    // wave 0 walks the sums (each lane a contiguous run of sub-blocks): no block-wide barrier until the result
+    if (threadIdx.x < 64) {
+        const int l = threadIdx.x;
+        const int per = (nsb_total + 63) >> 6;
+        const int lo = min(nsb_total, l * per), hi = min(nsb_total, lo + per);
+        double zpart = 0.0;
+        for (int i = lo; i < hi; ++i) zpart += sm.u.sbs[i];
+        const double zs = wave_sum_d(zpart);
+        const float inv = 1.0f / (float)zs;
+        double mine = 0.0;
+        for (int i = lo; i < hi; ++i) mine += sm.u.sbs[i] * (double)inv;
+        const double incl = wave_incl_scan(mine);
+        const double total = __longlong_as_double(
+            (long long)(((unsigned long long)(uint32_t)__builtin_amdgcn_readlane((int)((unsigned long long)__double_as_longlong(incl) >> 32), 63) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((int)__double_as_longlong(incl), 63)));
+        double run = shfl_up_d(incl, 1);  // exclusive: the sub-blocks before this lane's run
+        if (l == 0) run = 0.0;
+        const float target = u * (float)total;
+        int first = INT_MAX;
+        for (int i = lo; i < hi; ++i) {
+            const double nxt = run + sm.u.sbs[i] * (double)inv;
+            if ((float)nxt > target) {
+                first = i;
+                break;
+            }
+            run = nxt;
         }
-        run = nxt;
+        const unsigned long long hit = __ballot(first != INT_MAX);
+        if (l == 0) {
+            sm.sel_rem = INT_MAX;
+            sm.red_f[0] = inv;
+            sm.red_f[1] = target;
+        }
+        if (hit != 0ull && l == __ffsll((long long)hit) - 1) {
+            sm.sel_rem = first;
+            sm.red_d[0] = run;
+        }
     }
-    first = block_min_i(first, sm);
-    // exclusive running sum before sub-block `first`
-    double before = (first != INT_MAX && first >= lo && first < hi) ? run : 0.0;
-    const int owner = first == INT_MAX ? -1 : first / max(per, 1);
     __syncthreads();
-    if ((int)threadIdx.x == owner) sm.red_d[0] = before;
-    __syncthreads();
-    before = owner >= 0 ? sm.red_d[0] : 0.0;
+    const float inv = sm.red_f[0], target = sm.red_f[1];
+    const int first = sm.sel_rem;
+    double before = first != INT_MAX ? sm.red_d[0] : 0.0;
+    __syncthreads();  // (sel_rem and red_d are reused below)
     const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)c.row * G.allowed_stride : nullptr;
     const int nwords = (c.V + 31) >> 5;
     int cur_slice = -1;
@@ -2590,7 +2606,11 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
             sm.sel_bin = (int)(ex_pk & 4095ull);  // bin values ranked above the sub-bucket
             sm.sel_acc = ex_pk >> 12;            // and their mass
         }
-        if (threadIdx.x == 0) sm.sel_rem = 0;
+        if (threadIdx.x == 0) {
+            sm.sel_rem = 0;
+            sm.kmin = ~0u;
+            sm.kmax = 0u;
+        }
         __syncthreads();
         const int n_before = sm.sel_bin;
         const unsigned long long m_before = sm.sel_acc;
@@ -2598,10 +2618,21 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
             exact = false;  // the whole bin short of the target: the cut lies under the bin (streaming path)
         } else {
             // the sub-bucket's keys (bf16 inputs make many exact ties here), sorted descending
+            uint32_t kmin = ~0u, kmax = 0u;
             for (int q0 = 0; q0 < ntot; q0 += kBlock) {  // block-uniform trip count (append_key ballots)
                 const int q = q0 + threadIdx.x;
                 const float f = q < ntot ? sm.u.c.val[q] : -INFINITY;
-                append_key(q < ntot && bucket(f) == bstar, ord_key(f), sm);
+                const bool in = q < ntot && bucket(f) == bstar;
+                const uint32_t k = ord_key(f);
+                append_key(in, k, sm);
+                kmin = in ? min(kmin, k) : kmin;
+                kmax = in ? max(kmax, k) : kmax;
+            }
+            kmin = wave_reduce(kmin, [](uint32_t a, uint32_t b) { return min(a, b); });
+            kmax = wave_reduce(kmax, [](uint32_t a, uint32_t b) { return max(a, b); });
+            if (lane_id() == 0) {
+                atomicMin(&sm.kmin, kmin);
+                atomicMax(&sm.kmax, kmax);
             }
             __syncthreads();
             const int nbk = sm.sel_rem;
@@ -2609,7 +2640,8 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
             while (np < nbk) np <<= 1;
             for (int q = nbk + threadIdx.x; q < np; q += kBlock) sm.u.c.key[q] = 0u;
             __syncthreads();
-            sort_keys_desc(sm, np);
+            // one distinct value (bf16 ties): the keys, then the zero padding, are in order already
+            if (sm.kmin != sm.kmax) sort_keys_desc(sm, np);
             // ranks (blocked per thread) whose exclusive mass, above the sub-bucket included, is below the target
             const int per = (nbk + kBlock - 1) / kBlock;
             const int r0 = min(nbk, (int)threadIdx.x * per), r1 = min(nbk, r0 + per);
