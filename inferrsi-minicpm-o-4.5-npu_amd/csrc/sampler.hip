@@ -985,8 +985,9 @@ __device__ __forceinline__ int slice_prologue(const DevGroup& G, const Ctx& c, c
     return pen_bad;
 }
 
-// Division by the temperature: IEEE, corrected reciprocal, or (power-of-two divisor) one exact product.
-enum DivMode { kDivIeee = 0, kDivFast = 1, kDivPow2 = 2 };
+// Division by the temperature: the corrected reciprocal (divisors in [2^-16, 2^16], powers of two included: there
+// the product is exact and the correction zero), or IEEE division.
+enum DivMode { kDivIeee = 0, kDivFast = 1 };
 
 // One element of the row's pipeline with IEEE division, for the chunks the fast form does not cover.
 template <bool HF, bool COUNTS>
@@ -1049,18 +1050,18 @@ __device__ __forceinline__ void process_tile_t(const DevGroup& G, const Ctx& c, 
                 continue;
             }
             float y = x;
-            if (COUNTS || DIV != kDivPow2) slow |= !raw_in_range(x);  // one check covers every division below
-            if (HF) y = DIV == kDivPow2 ? y * rd : div_rn(y, d, rd);
+            slow |= !raw_in_range(x);  // one check covers every division below
+            if (HF) y = div_rn(y, d, rd);
             if (COUNTS) {
                 const PenEntry pe = sm.pen[n];
                 const float q = div_rn(y, pe.a, pe.ra);
                 y = y < 0.f ? y * pe.a : q;
                 y = (y - pe.fn) - pe.pn;
             }
-            if (!HF) y = DIV == kDivPow2 ? y * rd : div_rn(y, d, rd);
+            if (!HF) y = div_rn(y, d, rd);
             f[e] = y;
         }
-        if (DIV != kDivIeee || COUNTS) {
+        {
             if (slow) {
 #pragma unroll
                 for (int e = 0; e < E; ++e) {
@@ -1077,9 +1078,7 @@ __device__ __forceinline__ void process_tile_t(const DevGroup& G, const Ctx& c, 
 template <int ES, bool HF, bool COUNTS>
 __device__ __forceinline__ void process_tile_d(const DevGroup& G, const Ctx& c, const Geo& g, const RawTile<ES>& R,
                                                Tile& T, const Smem& sm, int mode) {
-    if (mode == kDivPow2)
-        process_tile_t<ES, HF, COUNTS, kDivPow2>(G, c, g, R, T, sm);
-    else if (mode == kDivFast)
+    if (mode == kDivFast)
         process_tile_t<ES, HF, COUNTS, kDivFast>(G, c, g, R, T, sm);
     else
         process_tile_t<ES, HF, COUNTS, kDivIeee>(G, c, g, R, T, sm);
@@ -1091,9 +1090,7 @@ __device__ __forceinline__ void finish_tile(const DevGroup& G, const Ctx& c, con
                                             const Preload& P, Tile& T, Smem& sm) {
     constexpr int E = 16 / ES;
     const int pen_bad = slice_prologue(G, c, g, E, P, sm);
-    // pow2: d = 2^k, so x * 2^-k is x / d correctly rounded for every x
-    const bool pow2 = (__float_as_uint(c.tdiv) & 0x807fffffu) == 0u && c.tdiv >= 0x1p-126f && c.tdiv <= 0x1p126f;
-    int mode = pow2 ? kDivPow2 : divisor_in_range(c.tdiv) ? kDivFast : kDivIeee;
+    int mode = divisor_in_range(c.tdiv) ? kDivFast : kDivIeee;
     if (c.counts && pen_bad) mode = kDivIeee;
     if (c.hf) {
         if (c.counts)
