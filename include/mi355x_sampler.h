@@ -124,9 +124,9 @@ const char* mis_last_error(void);
  * be zero-filled once when allocated; every launch leaves it zeroed again for the next. */
 size_t mis_workspace_bytes(const MisGroup* groups, int n_groups);
 
-/* The fused pipeline + draw (+ optional state update) for every row of every group: one kernel launch, plus a
- * second one when a group can hold top-p rows without top-k (it re-reads only the rows whose nucleus the first
- * pass could not settle).  Calls that share a workspace must be ordered on one stream. */
+/* The fused pipeline + draw (+ optional state update) for every row of every group: one kernel launch (a top-p
+ * row without top-k whose nucleus the slices' candidates cannot hold resolves its boundary bin inside it).  Calls
+ * that share a workspace must be ordered on one stream. */
 int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t workspace_bytes, void* stream);
 
 /* out[i] = U[0,1) of (seeds[i], steps[i], row_ids[i]) under MIS_RNG_COUNTER (row_ids ignored) or
