@@ -438,15 +438,22 @@ __device__ __forceinline__ T wave_reduce(T x, Op op) {
     return x;
 }
 
-// Inclusive scan over the wave's lanes.
+// A DPP move (lanes without a source in the pattern, or in rows outside ROW_MASK, read 0).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+
+// Inclusive scan over the wave's lanes, all in DPP moves: Hillis-Steele inside each row of 16 lanes (row_shr 1, 2,
+// 4, 8), then the row totals (row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3).
 template <class T>
 __device__ __forceinline__ T wave_incl_scan(T x) {
-    const int l = lane_id();
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const T y = shfl_up_d(x, o);
-        if (l >= o) x += y;
-    }
+    x += Lanes<T>::mv(x, dpp_or_zero<0x111, 0xF>);
+    x += Lanes<T>::mv(x, dpp_or_zero<0x112, 0xF>);
+    x += Lanes<T>::mv(x, dpp_or_zero<0x114, 0xF>);
+    x += Lanes<T>::mv(x, dpp_or_zero<0x118, 0xF>);
+    x += Lanes<T>::mv(x, dpp_or_zero<0x142, 0xA>);
+    x += Lanes<T>::mv(x, dpp_or_zero<0x143, 0xC>);
     return x;
 }
 
@@ -822,21 +829,29 @@ __device__ __forceinline__ int build_counts(const DevGroup& G, const Ctx& c, int
             }
         }
     } else {
-        for (int b0 = 0; b0 < W || b0 == 0; b0 += kBlock * 8) {
-            int64_t h[8];
+        // one loop per id width, loads from clamped indices (a load under a branch would be waited for at the join)
+        auto scan = [&](auto id_type) {
+            using Id = decltype(id_type);
+            const Id* hp = (const Id*)hrow;
+            for (int b0 = 0; b0 < W || b0 == 0; b0 += kBlock * 8) {
+                int64_t h[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int i = b0 + u * kBlock + threadIdx.x;
-                h[u] = i < W ? (G.hist_i64 ? ((const int64_t*)hrow)[i] : (int64_t)((const int32_t*)hrow)[i])
-                             : (int64_t)-1;
-            }
-            if (b0 == 0) {
-                bad = clear_counts(G, c, words, sm);
-                __syncthreads();
-            }
+                for (int u = 0; u < 8; ++u) h[u] = (int64_t)hp[max(min(b0 + u * kBlock + (int)threadIdx.x, W - 1), 0)];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) count_id(sm, h[u], base, lo, hi);
-        }
+                for (int u = 0; u < 8; ++u)
+                    if (b0 + u * kBlock + (int)threadIdx.x >= W) h[u] = -1;
+                if (b0 == 0) {
+                    bad = clear_counts(G, c, words, sm);
+                    __syncthreads();
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) count_id(sm, h[u], base, lo, hi);
+            }
+        };
+        if (G.hist_i64)
+            scan(int64_t{});
+        else
+            scan(int32_t{});
     }
     return __syncthreads_or(bad);
 }
@@ -1235,11 +1250,7 @@ __device__ __forceinline__ void pick_count_bin(int rem, Smem& sm) {
             h[r] = sm.hcnt[255 - (4 * l + r)];
             sum += (int)h[r];
         }
-        int incl = sum;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = shfl_up_d(incl, o);
-            if (l >= o) incl += y;
-        }
+        const int incl = wave_incl_scan(sum);
         int before = incl - sum;
         for (int r = 0; r < 4; ++r) {
             if (before < rem && rem <= before + (int)h[r]) {
@@ -1319,11 +1330,7 @@ __device__ __forceinline__ float stream_mass(const DevGroup& G, const Ctx& c, Sm
                 hc[r] = sm.hcnt[255 - (4 * l + r)];
                 sum += hm[r];
             }
-            unsigned long long incl = sum;
-            for (int o = 1; o < 64; o <<= 1) {
-                const unsigned long long y = shfl_up_d(incl, o);
-                if (l >= o) incl += y;
-            }
+            const unsigned long long incl = wave_incl_scan(sum);
             unsigned long long before = acc + (incl - sum);
             int mine = -1;
             unsigned long long mine_before = 0ull;
@@ -1940,13 +1947,7 @@ __device__ __forceinline__ int sub_block_draw(const DevGroup& G, const Ctx& c, S
                 }
             }
             // wave-level exclusive scan
-            double incl = mine2;
-            for (int o = 1; o < 64; o <<= 1) {
-                const double y = shfl_up_d(incl, o);
-                if (lane_id() >= o) incl += y;
-            }
-            double r = before + incl - mine2;
-            (void)r;
+            const double incl = wave_incl_scan(mine2);
             double ex = shfl_up_d(incl, 1);
             if (lane_id() == 0) ex = 0.0;
             double rr = before + ex;
@@ -2019,11 +2020,7 @@ __device__ __forceinline__ int gather_cands(const Ctx& c, Smem& sm, const RowWs&
     if (threadIdx.x < 64) {
         const int l = threadIdx.x;
         const int x = l < c.S ? sm.summ[l].ncand : 0;
-        int incl = x;
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = shfl_up_d(incl, o);
-            if (l >= o) incl += y;
-        }
+        const int incl = wave_incl_scan(x);
         sm.coff[l] = incl - x;
         if (l == 63) sm.coff[kMaxSlices] = incl;
         if (l == 0) sm.sel_rem = 0;  // key counter
