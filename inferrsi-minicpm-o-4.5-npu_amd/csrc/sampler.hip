@@ -352,22 +352,34 @@ __device__ __forceinline__ int fresh_tid() {
 }
 __device__ __forceinline__ int fresh_lane() { return fresh_tid() & 63; }
 
-// Cross-lane moves.  Each computes its own lane arithmetic, so no lane index is shared (and kept live) across the
-// kernel: xor offsets 1, 2 and 8 are DPP moves, 4 and 16 ds_swizzle's bit-mask mode (the pattern is an
-// immediate), the others ds_bpermute.
+// Cross-lane moves.  The fixed xor partners are all VALU moves: DPP for 1 and 2 (quad permutes), 4 (row half
+// mirror, then a quad reversal) and 8 (rotate by 8 in a row of 16), gfx950's permlane swaps for 16 and 32.  The
+// dynamic ones use ds_bpermute and compute their own lane arithmetic, so no lane index is shared (and kept live)
+// across the kernel.
+__device__ __forceinline__ uint32_t lane_mbcnt() {
+    return __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
 template <int O>
 __device__ __forceinline__ uint32_t xor_lane(uint32_t x) {
     static_assert(O >= 1 && O <= 32 && (O & (O - 1)) == 0, "power-of-two offset");
-    if constexpr (O == 1)
+    if constexpr (O == 1) {
         return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-    else if constexpr (O == 2)
+    } else if constexpr (O == 2) {
         return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-    else if constexpr (O == 8)
+    } else if constexpr (O == 4) {
+        const int m = __builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false);  // lane i <- 7 - i (in 8)
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, m, 0x1B, 0xF, 0xF, false);      // then i <- 3 - i (in 4)
+    } else if constexpr (O == 8) {
         return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false);  // row_ror:8 = lane ^ 8
-    else if constexpr (O == 32)
-        return (uint32_t)__builtin_amdgcn_ds_bpermute((fresh_lane() ^ 32) << 2, (int)x);
-    else
-        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x1f | (O << 10));  // lane ^ O within 32 lanes
+    } else if constexpr (O == 16) {
+        // odd rows of the first result hold the even rows' values and even rows of the second the odd rows'
+        const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return (lane_mbcnt() & 16u) ? r[0] : r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return lane_mbcnt() < 32u ? r[1] : r[0];
+    }
 }
 
 __device__ __forceinline__ uint32_t xor_lane_dyn(uint32_t x, int o) {
