@@ -2534,6 +2534,11 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
     }
     __syncthreads();
     const Pending P = sm.held;
+    if (w.tile != nullptr) {  // the processed values, for the draw inside one sub-block (first: they drain meanwhile)
+        float* tl = w.tile + (int64_t)slice * kNV * kBlock + threadIdx.x;
+#pragma unroll
+        for (int q = 0; q < kNV; ++q) pub_st(&tl[q * kBlock], T.v[q]);
+    }
     // everything above the boundary bin survives: its sums per sub-block; the bin's values go to the finaliser
     const double part = tile_sub_sums<ES>(T, P.m, P.hi_v, sm);
     int nhi = 0;
@@ -2543,11 +2548,6 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
     const double hi_mass = block_sum_d(part, sm);
     nhi = block_sum_i(nhi, sm);
     if ((int)threadIdx.x < NSB) pub_st(&w.sb[(int64_t)slice * kMaxSB + threadIdx.x], sm.sbw[threadIdx.x]);
-    if (w.tile != nullptr) {  // the processed values, for the draw inside one sub-block
-        float* tl = w.tile + (int64_t)slice * kNV * kBlock + threadIdx.x;
-#pragma unroll
-        for (int q = 0; q < kNV; ++q) pub_st(&tl[q * kBlock], T.v[q]);
-    }
     const int run = publish_range<ES>(T, geo, P.lo_v, P.hi_v, w.cand + (int64_t)slice * kCapSlice, sm);
     if (threadIdx.x == 0) {
         SliceSummary& s = w.summ[slice];
