@@ -1579,34 +1579,6 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Ctx& c, in
     }
 }
 
-// The c-th largest (1 <= c <= 256) of the 256 per-thread values v: a most-significant-bit-first radix select
-// over their order keys in wave 0 (4 keys per lane), counting each digit's keys with ballots.
-__device__ __forceinline__ float block_kth_of_256(float v, int c, Smem& sm) {
-    sm.tmax[threadIdx.x] = v;
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        uint32_t k[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) k[r] = ord_key(sm.tmax[4 * lane + r]);
-        uint32_t prefix = 0u;
-        int need = c;
-        for (int bit = 31; bit >= 0; --bit) {
-            const uint32_t hm = ~0u << bit;
-            const uint32_t want = prefix | (1u << bit);
-            int cnt = 0;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) cnt += __popcll(__ballot((k[r] & hm) == want));
-            if (cnt >= need)
-                prefix = want;
-            else
-                need -= cnt;
-        }
-        if (lane == 0) sm.sel_tau = key_float(prefix);
-    }
-    __syncthreads();
-    return sm.sel_tau;
-}
 
 // Appends key to sm.u.c.key at sm.sel_rem where pred holds (any order): one LDS atomic per wave, positions
 // within the wave from the ballot.
@@ -1797,6 +1769,17 @@ __device__ __forceinline__ void sort_keys_desc(Smem& sm, int np) {
         default: sort_n<2048>(sm); break;
     }
 }
+
+// The c-th largest (1 <= c <= 256) of the 256 per-thread values v: their order keys sorted by the bitonic network
+// (all four waves, one key per lane), then read at rank c - 1.  Uses sm.u (the slice's count table is spent).
+__device__ __forceinline__ float block_kth_of_256(float v, int c, Smem& sm) {
+    __syncthreads();  // the union may still be in use
+    sm.u.c.key[threadIdx.x] = ord_key(v);
+    __syncthreads();
+    sort_n<kBlock>(sm);  // ends with a barrier
+    return key_float(sm.u.c.key[c - 1]);
+}
+
 
 // The top-k / top-p threshold from the sorted candidate keys (vocabulary counts n >= ...).  z_full is the
 // full-row normaliser (hf order); omni normalises over the top k (engine/talker_sampler.py:112,129).
