@@ -956,23 +956,26 @@ __device__ __forceinline__ void issue_tile(const Geo& g, RawTile<ES>& R) {
 // The slice's other inputs, loaded right after its tile (before the row's parameters are known): the allowed
 // bits of the words covering it, limited to [lo, hi), and the first kBlock * 4 int4 of the row's history.
 struct Preload {
-    uint32_t mw[2];
+    uint32_t mw[2];    // the slice's range bits of the two words
+    uint32_t mraw[2];  // the row's mask words as loaded (used when the row has a mask)
     int4 h[4];
-    bool hvec;
+    bool hvec, masked;
 };
 
 __device__ __forceinline__ void preload(const DevGroup& G, int row, const Geo& g, Preload& P, bool history = true) {
     const uint32_t* mrow = gp(G.allowed) ? gp(G.allowed) + (int64_t)row * G.allowed_stride : nullptr;
+    P.masked = mrow != nullptr;
     const int wb = g.first >> 5;  // arithmetic shift: first may be negative in slice 0
     const int wmax = (G.vocab - 1) >> 5;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int gw = wb + (int)threadIdx.x + u * kBlock;
         const int a = g.lo - 32 * gw, b = g.hi - 32 * gw;
-        uint32_t m = (a <= 0 ? ~0u : a >= 32 ? 0u : ~0u << a) & (b >= 32 ? ~0u : b <= 0 ? 0u : (1u << b) - 1u);
-        // unconditional load of a clamped word (words outside [lo, hi) are masked off by m anyway)
-        if (mrow != nullptr) m &= mrow[min(max(gw, 0), wmax)];
-        P.mw[u] = m;
+        P.mw[u] = (a <= 0 ? ~0u : a >= 32 ? 0u : ~0u << a) & (b >= 32 ? ~0u : b <= 0 ? 0u : (1u << b) - 1u);
+        // a clamped word (words outside [lo, hi) are masked off by mw), loaded with no branch around it (a row
+        // without a mask reads the tile's first word instead) and combined only where it is used: a load under a
+        // branch, or used at once, would be waited for together with the tile's loads before it
+        P.mraw[u] = *(mrow != nullptr ? mrow + min(max(gw, 0), wmax) : (const uint32_t*)g.base);
     }
     const char* hrow = gp(G.history) != nullptr && G.hist_len > 0 ? hist_row(G, row) : nullptr;
     P.hvec = history && hrow != nullptr && hist_vec(G, hrow);
@@ -995,7 +998,7 @@ __device__ __forceinline__ int slice_prologue(const DevGroup& G, const Ctx& c, c
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
         const int gw = wb + (int)threadIdx.x + u * kBlock;
-        mw[u] = P.mw[u];
+        mw[u] = P.masked ? P.mw[u] & P.mraw[u] : P.mw[u];
         if (eos >= 0 && (eos >> 5) == gw) mw[u] &= ~(1u << (eos & 31));
     }
     int pen_bad = 0;
@@ -2444,14 +2447,14 @@ __device__ __forceinline__ void resolve_bin(const DevGroup& G, const Ctx& c, con
 
 template <int ES>
 __device__ __forceinline__ void run_row(const DevGroup& G, const int row, const int slice, Smem& sm) {
-    // the row's parameters, then the slice's tile, mask words and history go out before any of them is used
-    RowParams q;
-    load_params(G, row, q);
+    // the slice's tile, mask words and history, then the row's parameters, go out before any of them is used
     const Geo geo = slice_geo_at<ES>(G, row, slice);
     RawTile<ES> R;
     issue_tile<ES>(geo, R);
     Preload P;
     preload(G, row, geo, P);
+    RowParams q;
+    load_params(G, row, q);
     Ctx c;
     init_ctx(G, row, slice, q, c);
     const RowWs w = row_ws(gp(G.ws) + (int64_t)row * G.ws_row_bytes, c.S, G.tiles != 0);
