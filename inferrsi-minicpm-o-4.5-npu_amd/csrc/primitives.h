@@ -138,25 +138,35 @@ __device__ __forceinline__ uint32_t rank_below(uint64_t b) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
 }
 
-// Workgroup scratch for the reductions below (one slot per wave).
-struct Red {
+// Workgroup scratch for the reductions below (one slot per wave, 16-byte aligned so that a thread reads all 16
+// partials with a few wide LDS loads).
+struct alignas(16) Red {
     double d[kWaves];
     unsigned long long u[kWaves];
+    float4 f4[kWaves];
     float f[kWaves];
     int32_t i[kWaves];
     int32_t j[kWaves];
 };
 
 // Workgroup reductions.  Each starts with a barrier (the scratch may still be read by the previous one) and ends
-// with every thread holding the result.
+// with every thread holding the result.  The 16 wave partials are combined in a fixed order.
+template <class T, int N>
+__device__ __forceinline__ void load_partials(const T (&src)[N], T (&dst)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) dst[i] = src[i];
+}
+
 __device__ __forceinline__ float block_max_f(float x, Red& r) {
     x = wave_reduce(x, [](float a, float b) { return fmaxf(a, b); });
     __syncthreads();
     if (lane_id() == 0) r.f[wave_id()] = x;
     __syncthreads();
-    float m = r.f[0];
+    float p[kWaves];
+    load_partials(r.f, p);
+    float m = p[0];
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) m = fmaxf(m, r.f[i]);
+    for (int i = 1; i < kWaves; ++i) m = fmaxf(m, p[i]);
     return m;
 }
 
@@ -165,9 +175,11 @@ __device__ __forceinline__ int block_min_i(int x, Red& r) {
     __syncthreads();
     if (lane_id() == 0) r.i[wave_id()] = x;
     __syncthreads();
-    int m = r.i[0];
+    int p[kWaves];
+    load_partials(r.i, p);
+    int m = p[0];
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) m = min(m, r.i[i]);
+    for (int i = 1; i < kWaves; ++i) m = min(m, p[i]);
     return m;
 }
 
@@ -176,9 +188,11 @@ __device__ __forceinline__ int block_max_i(int x, Red& r) {
     __syncthreads();
     if (lane_id() == 0) r.i[wave_id()] = x;
     __syncthreads();
-    int m = r.i[0];
+    int p[kWaves];
+    load_partials(r.i, p);
+    int m = p[0];
 #pragma unroll
-    for (int i = 1; i < kWaves; ++i) m = max(m, r.i[i]);
+    for (int i = 1; i < kWaves; ++i) m = max(m, p[i]);
     return m;
 }
 
@@ -187,9 +201,11 @@ __device__ __forceinline__ int block_sum_i(int x, Red& r) {
     __syncthreads();
     if (lane_id() == 0) r.i[wave_id()] = x;
     __syncthreads();
+    int p[kWaves];
+    load_partials(r.i, p);
     int m = 0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) m += r.i[i];
+    for (int i = 0; i < kWaves; ++i) m += p[i];
     return m;
 }
 
@@ -198,9 +214,11 @@ __device__ __forceinline__ double block_sum_d(double x, Red& r) {
     __syncthreads();
     if (lane_id() == 0) r.d[wave_id()] = x;
     __syncthreads();
+    double p[kWaves];
+    load_partials(r.d, p);
     double m = 0.0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) m += r.d[i];
+    for (int i = 0; i < kWaves; ++i) m += p[i];
     return m;
 }
 
@@ -209,35 +227,65 @@ __device__ __forceinline__ unsigned long long block_sum_u(unsigned long long x, 
     __syncthreads();
     if (lane_id() == 0) r.u[wave_id()] = x;
     __syncthreads();
+    unsigned long long p[kWaves];
+    load_partials(r.u, p);
     unsigned long long m = 0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) m += r.u[i];
+    for (int i = 0; i < kWaves; ++i) m += p[i];
+    return m;
+}
+
+// Four float maxima at once (one barrier pair).
+__device__ __forceinline__ float4 block_max4(float4 v, Red& r) {
+    auto mx = [](float a, float b) { return fmaxf(a, b); };
+    v.x = wave_reduce(v.x, mx);
+    v.y = wave_reduce(v.y, mx);
+    v.z = wave_reduce(v.z, mx);
+    v.w = wave_reduce(v.w, mx);
+    __syncthreads();
+    if (lane_id() == 0) r.f4[wave_id()] = v;
+    __syncthreads();
+    float4 p[kWaves];
+    load_partials(r.f4, p);
+    float4 m = p[0];
+#pragma unroll
+    for (int i = 1; i < kWaves; ++i) {
+        m.x = fmaxf(m.x, p[i].x);
+        m.y = fmaxf(m.y, p[i].y);
+        m.z = fmaxf(m.z, p[i].z);
+        m.w = fmaxf(m.w, p[i].w);
+    }
     return m;
 }
 
 // Max of (value, first index): the largest value, and among equal values the smallest index.
 __device__ __forceinline__ void block_argmax(float& v, int& idx, Red& r) {
     auto better = [](float a, int ia, float b, int ib) { return a > b || (a == b && ia < ib); };
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        float ov;
-        int oi;
-        if (o == 32) { ov = shfl_xor<32>(v); oi = shfl_xor<32>(idx); }
-        else if (o == 16) { ov = shfl_xor<16>(v); oi = shfl_xor<16>(idx); }
-        else if (o == 8) { ov = shfl_xor<8>(v); oi = shfl_xor<8>(idx); }
-        else if (o == 4) { ov = shfl_xor<4>(v); oi = shfl_xor<4>(idx); }
-        else if (o == 2) { ov = shfl_xor<2>(v); oi = shfl_xor<2>(idx); }
-        else { ov = shfl_xor<1>(v); oi = shfl_xor<1>(idx); }
-        if (better(ov, oi, v, idx)) { v = ov; idx = oi; }
-    }
+    auto step = [&](float ov, int oi) {
+        if (better(ov, oi, v, idx)) {
+            v = ov;
+            idx = oi;
+        }
+    };
+    step(shfl_xor<32>(v), shfl_xor<32>(idx));
+    step(shfl_xor<16>(v), shfl_xor<16>(idx));
+    step(shfl_xor<8>(v), shfl_xor<8>(idx));
+    step(shfl_xor<4>(v), shfl_xor<4>(idx));
+    step(shfl_xor<2>(v), shfl_xor<2>(idx));
+    step(shfl_xor<1>(v), shfl_xor<1>(idx));
     __syncthreads();
-    if (lane_id() == 0) { r.f[wave_id()] = v; r.j[wave_id()] = idx; }
+    if (lane_id() == 0) r.f4[wave_id()] = make_float4(v, __int_as_float(idx), 0.f, 0.f);
     __syncthreads();
-    v = r.f[0];
-    idx = r.j[0];
+    float4 p[kWaves];
+    load_partials(r.f4, p);
+    v = p[0].x;
+    idx = __float_as_int(p[0].y);
 #pragma unroll
     for (int i = 1; i < kWaves; ++i)
-        if (better(r.f[i], r.j[i], v, idx)) { v = r.f[i]; idx = r.j[i]; }
+        if (better(p[i].x, __float_as_int(p[i].y), v, idx)) {
+            v = p[i].x;
+            idx = __float_as_int(p[i].y);
+        }
 }
 
 // Exclusive prefix over the workgroup in thread order, and the total (integer types: the subtraction is exact).
@@ -248,12 +296,15 @@ __device__ __forceinline__ T block_excl_scan(T x, T& total, T* scratch /* kWaves
     __syncthreads();
     if (lane_id() == 63) scratch[wave_id()] = incl;
     __syncthreads();
+    T p[kWaves];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) p[i] = scratch[i];
     T off = T(0);
     total = T(0);
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) {
-        if (i < wave_id()) off += scratch[i];
-        total += scratch[i];
+        off += (i < wave_id()) ? p[i] : T(0);
+        total += p[i];
     }
     return off + incl - x;
 }

@@ -41,17 +41,18 @@ constexpr int kMaxGroups = 4;
 constexpr int kMaxSlices = 64;
 constexpr int kMaxRows = 16384;
 constexpr int kMaxVocab = 1 << 21;               // token ids fit the 21-bit keys of the draw
-constexpr int kTileElems = 40;                   // elements per thread of a slice, at most
+constexpr int kRounds = 5;                       // 16-byte chunks per thread of a slice, at most
+constexpr int kTileElems = 40;                   // elements per thread of a slice, at most (bf16; fp32: 20)
 constexpr int kTileMax = kThreads * kTileElems;  // 40,960
 constexpr int kCntWords = kTileMax / 2;          // history counts, u16 pairs
 constexpr int kKeepWords = kTileMax / 32 + 3;    // keep bits of a slice (allowed, in range, not special)
 constexpr int kSpecCap = 2048;                   // specials of one slice
-constexpr int kCapWave = 256;                    // candidates one wave of a slice may publish
+constexpr int kCapWave = 512;                    // candidates one wave of a slice may publish
 constexpr int kCapSpecSeg = 512;                 // candidates among a slice's specials
 constexpr int kSegs = kWaves + 1;                // candidate segments of a slice: 16 waves + the specials
 constexpr int kCapRow = 12288;                   // candidates a finaliser gathers
 constexpr int kBins = 2048;                      // radix digit: 11 bits
-constexpr int kMaxSB = kWaves * 10;              // (wave, round) sub-blocks of a slice
+constexpr int kMaxSB = kWaves * kRounds;         // (wave, round) sub-blocks of a slice
 constexpr double kFx = 35184372088832.0;         // 2^45 fixed-point units of exp(q - max)
 constexpr int kLineBytes = 128;                  // a row's arrival word has a cache line of its own
 constexpr int64_t kHeaderBytes = 256;            // status word
@@ -245,14 +246,13 @@ __device__ __forceinline__ Row make_row(const DevGroup& G, int gi, int row, int 
     R.eos_rule = !censor ? kEosNormal
                          : (!R.hf ? kEosExcluded : ((R.filters && (topk || R.p_active)) ? kEosSelOnly : kEosExcluded));
     R.needz = R.mode == kNucleus || (R.mode == kTopK && R.hf && R.p_active);
-    // lanes of the slice that hold elements: a gate at half of them keeps the candidates near 2% of the slice
-    const int per_lane = (16 / G.es) * G.R;
-    const int lanes = (R.hi - R.lo + per_lane - 1) / per_lane;
+    // lane maxima per wave the gate keeps: the row's k, up to 64 (then the wave's own top k are all published), else
+    // twice the wave's expected share of the top k plus 8; 16 for top-p rows without top-k
+    const int span_w = 64 * (16 / G.es) * G.R;
     if (R.mode == kTopK)
-        R.c_gate = min(R.kk, 2 * R.kk / R.S + 64);
+        R.c_gate = R.kk <= 64 ? R.kk : min(48, (int)((2ll * R.kk * span_w + R.V - 1) / R.V) + 8);
     else
-        R.c_gate = min(1024, max(64, 9000 / R.S));
-    R.c_gate = max(1, min(R.c_gate, max(1, lanes / 2)));
+        R.c_gate = 16;
     return R;
 }
 
@@ -397,63 +397,6 @@ __device__ __forceinline__ void build_counts(const DevGroup& G, const Row& R, in
     __syncthreads();
 }
 
-// ------------------------------------------------------------------ radix selection
-
-// Scans keys of `bits` significant bits in descending (DESC) or ascending order and finds the first key at which
-// the cumulative weight reaches T (T >= 1).  src(f) calls f(key, weight) for this thread's elements (every thread
-// calls src; it may contain barriers).  Returns false when the total weight is below T; otherwise the key and
-// the weight of every key strictly before it in scan order.  Weights are integers, so the result does not depend
-// on the order of the LDS additions.
-template <bool DESC, class Src>
-__device__ __forceinline__ bool radix_find(Src&& src, unsigned long long T, int bits, Hist& h, uint32_t& key_out,
-                           unsigned long long& before_out) {
-    uint32_t prefix = 0;
-    int done = 0;
-    unsigned long long acc = 0;
-    while (done < bits) {
-        const int lb = min(11, bits - done);
-        const int shift = bits - done - lb;
-        const int nb = 1 << lb;
-        for (int b = threadIdx.x; b < kBins; b += kThreads) h.w[b] = 0ull;
-        __syncthreads();
-        const uint32_t pre = prefix;
-        const int above = shift + lb;
-        const bool check = done > 0;
-        src([&](uint32_t key, unsigned long long w) {
-            if (w == 0ull) return;
-            if (check && (key >> above) != pre) return;
-            atomicAdd(&h.w[(key >> shift) & (uint32_t)(nb - 1)], w);
-        });
-        __syncthreads();
-        const int s0 = 2 * (int)threadIdx.x, s1 = s0 + 1;
-        const int b0 = DESC ? nb - 1 - s0 : s0, b1 = DESC ? nb - 1 - s1 : s1;
-        const unsigned long long v0 = s0 < nb ? h.w[b0] : 0ull, v1 = s1 < nb ? h.w[b1] : 0ull;
-        unsigned long long tot;
-        const unsigned long long ex = block_excl_scan(v0 + v1, tot, h.scan);
-        if (threadIdx.x == 0) h.sel = -1;
-        __syncthreads();
-        if (s0 < nb && ex < T && T <= ex + v0) {
-            h.sel = b0;
-            h.before = ex;
-        } else if (s1 < nb && ex + v0 < T && T <= ex + v0 + v1) {
-            h.sel = b1;
-            h.before = ex + v0;
-        }
-        __syncthreads();
-        const int sel = h.sel;
-        const unsigned long long bf = h.before;
-        __syncthreads();
-        if (sel < 0) return false;
-        prefix = (prefix << lb) | (uint32_t)sel;
-        done += lb;
-        T -= bf;
-        acc += bf;
-    }
-    key_out = prefix;
-    before_out = acc;
-    return true;
-}
-
 // ------------------------------------------------------------------ cross-workgroup protocol
 //
 // A slice publishes with plain stores (the CU's L1 writes through to the XCD's L2), waits until they are
@@ -559,45 +502,73 @@ __device__ __forceinline__ uint32_t chunk_keep(const Lds& L, int first, int c) {
     return (uint32_t)(w >> sh) & ((1u << E) - 1u);
 }
 
-// The specials of a slice: processed value of each distinct history id (and of the EOS when it ranks but is not
-// drawn), their elements cleared from the keep bits.
-__device__ __forceinline__ void build_specials(const DevGroup& G, const Row& R, int first, Lds& L) {
-    const int eos = G.eos;
-    const bool eos_here = eos >= R.lo && eos < R.hi && R.eos_rule != kEosNormal;
-    if (R.pen) {
-        build_counts(G, R, first, kTileMax, R.lo, R.hi, true, eos_here ? eos : -1, L);
+// The first kThreads * 4 ids of the row's history, loaded with the tile (thread t: ids 4t .. 4t + 3).
+struct HistPre {
+    int32_t h[4];  // ids outside int32 are outside every vocabulary: -1
+};
+
+__device__ __forceinline__ void preload_history(const DevGroup& G, int row, HistPre& P) {
+    const int W = G.hist_len;
+    const char* hrow = G.history ? hist_row(G, row) : nullptr;
+    if (hrow && !G.hist_i64 && (((uintptr_t)hrow & 15) == 0) && W >= 4 * kThreads) {
+        const int4 v = gp((const int4*)hrow)[threadIdx.x];
+        P.h[0] = v.x;
+        P.h[1] = v.y;
+        P.h[2] = v.z;
+        P.h[3] = v.w;
     } else {
-        if (threadIdx.x == 0) L.nspec = 0;
-        __syncthreads();
-    }
-    const int nh = min(L.nspec, kSpecCap);
-    if (threadIdx.x == 0) {
-        if (L.nspec + (eos_here ? 1 : 0) > kSpecCap) L.flags |= kRecOverflow;
-        if (eos_here) {
-            clear_keep_bit(L, first, eos);
-            if (R.eos_rule == kEosSelOnly && nh < kSpecCap) {
-                L.spec[nh].j = eos;
-                L.spec[nh].sel = 1;
-                L.nspec = nh + 1;
-            }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = 4 * (int)threadIdx.x + u;
+            int64_t v = -1;
+            if (hrow && i < W) v = G.hist_i64 ? gp((const int64_t*)hrow)[i] : (int64_t)gp((const int32_t*)hrow)[i];
+            P.h[u] = (v >= 0 && v < INT_MAX) ? (int32_t)v : -1;
         }
     }
-    __syncthreads();
-    const int ns = min(L.nspec, kSpecCap);
-    for (int i = threadIdx.x; i < ns; i += kThreads) {
-        const int j = L.spec[i].j;
-        const int n = R.pen ? count_at(L, j - first) : 0;
-        L.spec[i].n = n;
-        if (!L.spec[i].sel) clear_keep_bit(L, first, j);
-        const float x = G.es == 2 ? load_elem<2>(G, R.row, j) : load_elem<4>(G, R.row, j);
-        L.spec[i].q = elem_q(R, G, x, n, allowed_bit(G, R.row, j), j);
+}
+
+// Counts history id h (if it falls in [lo, hi)) and, on its first occurrence, lists it as a special.
+__device__ __forceinline__ void count_id(int64_t h, int first, int lo, int hi, int skip_id, Lds& L) {
+    const bool in = h >= lo && h < hi;
+    uint32_t old = 1u;
+    if (in) {
+        const int pos = (int)(h - first);
+        old = atomicAdd(&L.a.cnt[pos >> 1], 1u << (16 * (pos & 1)));
+        old = (old >> (16 * (pos & 1))) & 0xffffu;
     }
-    __syncthreads();
+    const bool first_seen = in && old == 0u && (int)h != skip_id;
+    const uint64_t bal = ballot(first_seen);
+    if (bal) {
+        const int leader = __ffsll((long long)bal) - 1;
+        int base = 0;
+        if (lane_id() == leader) base = atomicAdd(&L.nspec, __popcll(bal));
+        base = __builtin_amdgcn_readlane(base, leader);
+        const int slot = base + (int)rank_below(bal);
+        if (first_seen && slot < kSpecCap) {
+            L.spec[slot].j = (int)h;
+            L.spec[slot].sel = 0;
+        }
+    }
+}
+
+// The row's allowed word for keep word k of a slice whose keep words start at element jb (~0 without a mask).
+__device__ __forceinline__ uint32_t mask_word(const DevGroup& G, int row, int jb, int k, int nkw) {
+    if (k >= nkw) return 0u;
+    if (!G.allowed) return ~0u;
+    const int gw = (jb >> 5) + k;
+    return (gw >= 0 && gw < (G.vocab + 31) >> 5) ? gp(G.allowed)[(int64_t)row * G.allowed_stride + gw] : 0u;
+}
+
+__device__ __forceinline__ uint32_t range_bits(int j0, int lo, int hi) {
+    const int a = lo - j0, b = hi - j0;
+    const uint32_t lo_m = a <= 0 ? ~0u : (a >= 32 ? 0u : (~0u << a));
+    const uint32_t hi_m = b >= 32 ? ~0u : (b <= 0 ? 0u : ((1u << b) - 1u));
+    return lo_m & hi_m;
 }
 
 // Appends the lanes' (qf(), j) where pred holds to the wave's candidate segment (global); cnt is wave-uniform.
 template <class QF>
-__device__ __forceinline__ void append_cand(bool pred, QF&& qf, int j, unsigned long long* seg, int cap, int& cnt,
+__device__ __forceinline__ void append_cand(bool pred, QF&& qf, uint32_t j, unsigned long long* seg, int cap, int& cnt,
                                             int& flags) {
     const uint64_t b = ballot(pred);
     if (b == 0ull) return;
@@ -607,8 +578,7 @@ __device__ __forceinline__ void append_cand(bool pred, QF&& qf, int j, unsigned 
         cnt = cap;
         return;
     }
-    if (pred)
-        seg[cnt + (int)rank_below(b)] = ((unsigned long long)(uint32_t)j << 32) | __float_as_uint(qf());
+    if (pred) seg[cnt + (int)rank_below(b)] = ((unsigned long long)j << 32) | __float_as_uint(qf());
     cnt += n;
 }
 
@@ -621,8 +591,8 @@ __device__ __forceinline__ uint32_t mask_pair(uint32_t v, uint32_t kb, int d) {
 __device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
 
-// Element e (0..E-1) of a chunk held as raw words: the value in the tile's domain (raw logits for bf16,
-// processed values for fp32).
+// Element e (0..E-1) of a chunk held as raw words, in the tile's domain (raw logits for bf16, processed values
+// for fp32).
 template <int ES>
 __device__ __forceinline__ float tile_val(const uint4& v, int e) {
     if (ES == 2) {
@@ -638,28 +608,125 @@ __device__ __forceinline__ float to_q(const Row& R, float x) {
     return ES == 2 ? div_rn(x, R.rT) : x;
 }
 
-// The slice phase of one workgroup; true when it is the row's last to arrive (it then finalises the row).
+// A value g such that at least c lanes of the wave have lmax >= g, by bisection between the wave's smallest and
+// largest finite lane maxima (-inf when fewer than c lanes hold a finite value).  Any element among the wave's c
+// largest is >= g: c lane maxima are >= g, and an element below g is exceeded by all of them.
+__device__ __forceinline__ float wave_gate(float lmax, int c) {
+    const bool fin = lmax > -INFINITY;
+    if (__popcll(ballot(fin)) < c) return -INFINITY;
+    float lo = wave_reduce(fin ? lmax : INFINITY, [](float a, float b) { return fminf(a, b); });
+    float hi = wave_reduce(fin ? lmax : -INFINITY, [](float a, float b) { return fmaxf(a, b); });
+    for (int it = 0; it < 10; ++it) {
+        const float mid = 0.5f * lo + 0.5f * hi;
+        if (!(mid > lo && mid < hi)) break;
+        if (__popcll(ballot(lmax >= mid)) >= c)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2 };
+
+// One slice workgroup: loads, the row's pipeline on the tile, publication, arrival.  Returns kActFinalize in the
+// row's last workgroup to arrive (R then holds the row), kActForced in slice 0 of a row whose EOS is forced.
 template <int ES>
-__device__ __forceinline__ bool slice_phase(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L) {
+__device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int gi, int row, int slice, Lds& L,
+                                   Row& Rout) {
     constexpr int E = Geo<ES>::E;
-    constexpr int RMAX = kTileElems / E;  // 5 (bf16) or 10 (fp32)
+    constexpr int RMAX = kRounds;
     const int RR = G.R;
-    if (threadIdx.x == 0) L.flags = 0;
-    SliceRec* rec = (SliceRec*)rec_base(G, R.row, R.slice);
-    if (R.mode == kStream) return arrive(A, R, L);
-    const Geo<ES> geo = slice_geo<ES>(G, R.row, R.lo);
-    const int w = wave_id(), l = lane_id();
-    // the tile's loads first: everything below overlaps them
+    const int lo = slice * G.slice_len, hi = min(G.vocab, lo + G.slice_len);
+    const Geo<ES> geo = slice_geo<ES>(G, row, lo);
+    const int w = wave_id(), l = lane_id(), tid = threadIdx.x;
+    // every input load first (the tile, its bitmask words, the row's history); the row's parameters after
     uint4 t[RMAX];
 #pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-        t[r] = make_uint4(0u, 0u, 0u, 0u);
-        if (r < RR) t[r] = load_chunk<ES>(geo, (w * RR + r) * 64 + l, R.hi);
+    for (int r = 0; r < RMAX; ++r)
+        t[r] = r < RR ? load_chunk<ES>(geo, (w * RR + r) * 64 + l, hi) : make_uint4(0u, 0u, 0u, 0u);
+    const int tile_len = kThreads * E * RR;
+    const int jb = (geo.first >> 5) << 5;
+    const int nkw = min(kKeepWords, (geo.first + tile_len - jb + 31) / 32 + 1);
+    uint32_t mw[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) mw[u] = mask_word(G, row, jb, tid + u * kThreads, nkw);
+    HistPre hp;
+    preload_history(G, row, hp);
+    const Row R = make_row(G, gi, row, slice);
+    Rout = R;
+    if (R.mode == kSkip) {
+        if (slice == 0 && tid == 0 && G.tokens) gp(G.tokens)[row] = kPad;
+        return kActNone;
     }
-    build_keep(G, R.row, geo.first, kThreads * E * RR, R.lo, R.hi, L);
+    if (R.mode == kForced) return slice == 0 ? kActForced : kActNone;
+    SliceRec* rec = (SliceRec*)rec_base(G, R.row, R.slice);
+    if (R.mode == kStream) return arrive(A, R, L) ? kActFinalize : kActNone;
+
+    // keep bits (allowed and in range) and, with penalties, a cleared count table
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int k = tid + u * kThreads;
+        if (k < kKeepWords) L.keep[k] = mw[u] & range_bits(jb + 32 * k, lo, hi);
+    }
+    if (R.pen) {
+        uint4* cw = (uint4*)L.a.cnt;
+        for (int i = tid; i < (tile_len / 2 + 4) / 4; i += kThreads) cw[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (tid == 0) {
+        L.flags = 0;
+        L.nspec = 0;
+    }
+    if (tid < kMaxSB) L.sbfx[tid] = 0ull;
     __syncthreads();
-    build_specials(G, R, geo.first, L);
+    // the history: counts and first occurrences (specials); a censored EOS is taken out of the tile (and listed as a
+    // special when it ranks but is not drawn)
+    const int eos = G.eos;
+    const bool eos_here = eos >= lo && eos < hi && R.eos_rule != kEosNormal;
+    if (eos_here && tid == 0) {
+        clear_keep_bit(L, geo.first, eos);
+        if (R.eos_rule == kEosSelOnly) {
+            const int slot = atomicAdd(&L.nspec, 1);
+            L.spec[slot].j = eos;
+            L.spec[slot].sel = 1;
+        }
+    }
+    if (R.pen) {
+        const int skip = eos_here ? eos : -1;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) count_id(hp.h[u], geo.first, lo, hi, skip, L);
+        if (G.hist_len > 4 * kThreads) {
+            const char* hrow = hist_row(G, R.row);
+            for (int b = 4 * kThreads; b < G.hist_len; b += kThreads) {
+                const int i = b + tid;
+                const int64_t h = i < G.hist_len
+                                      ? (G.hist_i64 ? gp((const int64_t*)hrow)[i] : (int64_t)gp((const int32_t*)hrow)[i])
+                                      : -1;
+                count_id(h, geo.first, lo, hi, skip, L);
+            }
+        }
+    }
+    __syncthreads();
+    // specials: counts, out of the tile, their logits loaded (the loads land during pass 1)
     const int ns = min(L.nspec, kSpecCap);
+    if (tid == 0 && L.nspec > kSpecCap) L.flags |= kRecOverflow;
+    float sx[2];
+    bool sal[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kThreads;
+        sx[u] = 0.f;
+        sal[u] = false;
+        if (i < ns) {
+            const int j = L.spec[i].j;
+            const int n = R.pen ? count_at(L, j - geo.first) : 0;
+            L.spec[i].n = n;
+            if (!L.spec[i].sel) clear_keep_bit(L, geo.first, j);
+            sx[u] = load_elem<ES>(G, R.row, j);
+            sal[u] = allowed_bit(G, R.row, j);
+        }
+    }
+    __syncthreads();
 
     // pass 1: keep bits applied; lane max (and first argmax for greedy rows) in the tile's domain
     float lmax = -INFINITY;
@@ -695,16 +762,21 @@ __device__ __forceinline__ bool slice_phase(const KernelArgs& A, const DevGroup&
             }
         }
     }
-
-    // the slice's maxima, in the processed domain, specials included
+    // the specials' processed values
     float smax = -INFINITY, sdmax = -INFINITY;
     int sarg = INT_MAX;
-    for (int i = threadIdx.x; i < ns; i += kThreads) {
-        const float q = L.spec[i].q;
-        smax = fmaxf(smax, q);
-        if (!L.spec[i].sel && (q > sdmax || (q == sdmax && L.spec[i].j < sarg))) {
-            sdmax = q;
-            sarg = L.spec[i].j;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        const int i = tid + u * kThreads;
+        if (i < ns) {
+            const int j = L.spec[i].j;
+            const float q = elem_q(R, G, sx[u], L.spec[i].n, sal[u], j);
+            L.spec[i].q = q;
+            smax = fmaxf(smax, q);
+            if (!L.spec[i].sel && (q > sdmax || (q == sdmax && j < sarg))) {
+                sdmax = q;
+                sarg = j;
+            }
         }
     }
 
@@ -717,28 +789,30 @@ __device__ __forceinline__ bool slice_phase(const KernelArgs& A, const DevGroup&
             idx = sarg;
         }
         block_argmax(v, idx, L.red);
-        if (threadIdx.x == 0) {
+        if (tid == 0) {
             rec->mq = v;
             rec->mqd = v;
             rec->argmax = idx;
             rec->flags = L.flags;
         }
-        return arrive(A, R, L);
+        return arrive(A, R, L) ? kActFinalize : kActNone;
     }
 
-    const float tmax = block_max_f(lmax, L.red);  // tile max, tile domain
-    const float tmq = is_finite_f(tmax) ? to_q<ES>(R, tmax) : tmax;
-    const float mq = fmaxf(tmq, block_max_f(smax, L.red));
-    const float mqd = fmaxf(tmq, block_max_f(sdmax, L.red));
+    const float4 mx = block_max4(make_float4(lmax, smax, sdmax, -INFINITY), L.red);
+    const float tmq = is_finite_f(mx.x) ? to_q<ES>(R, mx.x) : mx.x;  // tile max, processed domain
+    const float mq = fmaxf(tmq, mx.y);
+    const float mqd = fmaxf(tmq, mx.z);
 
     if (R.mode == kFull) {
         const float mref = mqd;
-        if (threadIdx.x < kMaxSB) L.sbfx[threadIdx.x] = 0ull;
-        __syncthreads();
         // specials' exp into their sub-blocks (fixed point: independent of the order of the additions)
-        for (int i = threadIdx.x; i < ns; i += kThreads) {
-            const unsigned long long f = efx(L.spec[i].q, mref);
-            if (f) atomicAdd(&L.sbfx[(L.spec[i].j - geo.first) / E >> 6], f);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int i = tid + u * kThreads;
+            if (i < ns) {
+                const unsigned long long f = efx(L.spec[i].q, mref);
+                if (f) atomicAdd(&L.sbfx[(L.spec[i].j - geo.first) / E >> 6], f);
+            }
         }
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
@@ -757,42 +831,28 @@ __device__ __forceinline__ bool slice_phase(const KernelArgs& A, const DevGroup&
         __syncthreads();
         const int nsb = kWaves * RR;
         double* sbg = (double*)((char*)rec + kRecSbOff);
-        if (threadIdx.x < nsb) {
-            const double s = L.sb[threadIdx.x] + (double)L.sbfx[threadIdx.x] * (1.0 / kFx);
-            L.sb[threadIdx.x] = s;
-            sbg[threadIdx.x] = s;
+        double sv = 0.0;
+        if (tid < nsb) {
+            sv = L.sb[tid] + (double)L.sbfx[tid] * (1.0 / kFx);
+            sbg[tid] = sv;
         }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double z = 0.0;
-            for (int k = 0; k < nsb; ++k) z += L.sb[k];
+        const double z = block_sum_d(sv, L.red);
+        if (tid == 0) {
             rec->mq = mq;
             rec->mqd = mqd;
             rec->mref = mref;
             rec->z = z;
             rec->flags = L.flags;
         }
-        return arrive(A, R, L);
+        return arrive(A, R, L) ? kActFinalize : kActNone;
     }
 
-    // top-k and top-p rows: the gate is the c-th largest lane maximum, so the slice's top c elements are all >= it
-    uint32_t gkey = 0u;
-    unsigned long long gbefore = 0ull;
-    const uint32_t mykey = ord_key(lmax);
-    const bool gfound = radix_find<true>(
-        [&](auto&& f) {
-            if (lmax > -INFINITY) f(mykey, 1ull);
-        },
-        (unsigned long long)R.c_gate, 32, L.h, gkey, gbefore);
-    // fewer finite lane maxima than c: every finite element is published
-    const float gate = gfound ? key_float(gkey) : -INFINITY;
+    // top-k and top-p rows: per-wave gates; every element of the wave at or above its gate is published
+    const float gate = wave_gate(lmax, R.c_gate);
     const float gate_q = (gate > -INFINITY) ? to_q<ES>(R, gate) : -INFINITY;
-    int flags = 0;
-    if (!gfound) flags |= kRecGateInf;
-
     unsigned long long* segs = (unsigned long long*)((char*)rec + kRecCandOff);
     unsigned long long* myseg = segs + (int64_t)w * kCapWave;
-    int cnt = 0;
+    int cnt = 0, flags = 0;
     double zacc = 0.0;
     const float mref = mq;
 #pragma unroll
@@ -803,93 +863,240 @@ __device__ __forceinline__ bool slice_phase(const KernelArgs& A, const DevGroup&
         for (int e = 0; e < E; ++e) {
             const float x = tile_val<ES>(t[r], e);
             const bool pred = x >= gate && x > -INFINITY;
+            const uint32_t j = (uint32_t)(geo.first + c * E + e);
             if (R.needz) {
                 const float q = to_q<ES>(R, x);
                 if (q > -INFINITY) zacc += (double)exp_acc(q - mref);
-                append_cand(pred, [&] { return q; }, geo.first + c * E + e, myseg, kCapWave, cnt, flags);
+                append_cand(pred, [&] { return q; }, j, myseg, kCapWave, cnt, flags);
             } else {
-                append_cand(pred, [&] { return to_q<ES>(R, x); }, geo.first + c * E + e, myseg, kCapWave, cnt, flags);
+                append_cand(pred, [&] { return to_q<ES>(R, x); }, j, myseg, kCapWave, cnt, flags);
             }
         }
     }
+    if (R.needz) zacc = wave_reduce(zacc, [](double a, double b) { return a + b; });
+    __syncthreads();
     if (l == 0) {
         L.segoff[w] = cnt;
+        L.red.f[w] = gate_q;
+        L.red.d[w] = zacc;
         if (flags) atomicOr(&L.flags, flags);
     }
-    // specials at or above the gate: segment kWaves, written by wave 0
+    __syncthreads();
+    float gs = -INFINITY;
+    double z = 0.0;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        gs = fmaxf(gs, L.red.f[i]);
+        z += L.red.d[i];
+    }
+    // specials at or above their wave's gate: segment kWaves, written by wave 0
     if (w == 0) {
         int scnt = 0, sflags = 0;
         unsigned long long* sseg = segs + (int64_t)kWaves * kCapWave;
+        double sz = 0.0;
         for (int b = 0; b < ns; b += 64) {
             const int i = b + l;
             const bool in = i < ns;
             const float q = in ? L.spec[i].q : -INFINITY;
-            const bool pred = in && q >= gate_q && q > -INFINITY;
-            const uint64_t bal = ballot(pred);
-            if (!bal) continue;
-            const uint32_t id = in ? ((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) : 0u;
-            if (scnt + __popcll(bal) > kCapSpecSeg) {
-                sflags |= kRecOverflow;
-                break;
-            }
-            if (pred) sseg[scnt + (int)rank_below(bal)] = ((unsigned long long)id << 32) | __float_as_uint(q);
-            scnt += __popcll(bal);
+            const int j = in ? L.spec[i].j : 0;
+            const int sw = in ? ((j - geo.first) / (E * RR * 64)) : 0;
+            const bool pred = in && q >= L.red.f[sw] && q > -INFINITY;
+            if (R.needz && in && q > -INFINITY) sz += (double)exp_acc(q - mref);
+            const uint32_t id = (uint32_t)j | ((in && L.spec[i].sel) ? kSelOnlyBit : 0u);
+            append_cand(pred, [&] { return q; }, id, sseg, kCapSpecSeg, scnt, sflags);
         }
+        sz = wave_reduce(sz, [](double a, double b) { return a + b; });
         if (l == 0) {
-            L.segoff[kWaves] = scnt;
-            if (sflags) atomicOr(&L.flags, sflags);
+            rec->ncand[kWaves] = scnt;
+            rec->mq = mq;
+            rec->mqd = mqd;
+            rec->gate = gs;
+            rec->mref = mref;
+            rec->z = z + sz;
+            rec->flags = L.flags | sflags | (gs > -INFINITY ? 0 : kRecGateInf);
         }
     }
-    double sz = 0.0;
-    if (R.needz) {
-        for (int i = threadIdx.x; i < ns; i += kThreads) {
-            const float q = L.spec[i].q;
-            if (q > -INFINITY) sz += (double)exp_acc(q - mref);
-        }
-    }
-    const double z = R.needz ? block_sum_d(zacc + sz, L.red) : 0.0;
-    __syncthreads();
-    if (threadIdx.x < kSegs) rec->ncand[threadIdx.x] = L.segoff[threadIdx.x];
-    if (threadIdx.x == 0) {
-        rec->mq = mq;
-        rec->mqd = mqd;
-        rec->gate = gate_q;
-        rec->mref = mref;
-        rec->z = z;
-        rec->flags = L.flags | flags;
-    }
-    return arrive(A, R, L);
+    if (tid < kWaves) rec->ncand[tid] = L.segoff[tid];
+    return arrive(A, R, L) ? kActFinalize : kActNone;
 }
 
-// ------------------------------------------------------------------ streaming source (finaliser fallback)
+// ------------------------------------------------------------------ the finaliser
+//
+// The finaliser asks questions of a set of elements: the candidates its slices published, gathered into LDS, or
+// the whole row, streamed in chunks with its processed values recomputed (history counts and keep bits rebuilt in
+// LDS for each chunk).  One visiting routine serves every question (maxima, the histogram rounds of a selection,
+// sums, the outputs), so the code that runs stays small.  Nothing here depends on the logits' dtype at compile
+// time.
 
-// Visits every element of [lo, hi) of the row with its processed value: f(q, j, drawable).  The range is taken
-// in chunks of the tile size, each with its history counts and keep bits rebuilt in LDS.  Every thread calls it.
-template <int ES, class F>
-__device__ __forceinline__ void stream_visit(const DevGroup& G, const Row& R, Lds& L, int lo, int hi, F&& f) {
-    const int chunk = kTileMax - 64;
-    for (int c0 = lo; c0 < hi; c0 += chunk) {
-        const int c1 = min(hi, c0 + chunk);
-        __syncthreads();
-        if (R.pen) {
-            build_counts(G, R, c0, c1 - c0, c0, c1, false, -1, L);
+__device__ __forceinline__ float load_logit(const DevGroup& G, int row, int j) {
+    const char* p = G.logits + ((int64_t)row * G.row_stride + j) * G.es;
+    return G.es == 2 ? __uint_as_float((uint32_t)*gp((const uint16_t*)p) << 16) : *gp((const float*)p);
+}
+
+__device__ __forceinline__ int slice_first(const DevGroup& G, int row, int lo) {
+    const char* rowp = G.logits + (int64_t)row * G.row_stride * G.es;
+    const uintptr_t lo_addr = (uintptr_t)(rowp + (int64_t)lo * G.es);
+    return lo - (int)((lo_addr & 15) / G.es);
+}
+
+enum : int { kSrcCands = 0, kSrcRow = 1 };
+enum : int { kJobStats = 0, kJobHist, kJobSums, kJobSurvMax, kJobSurvSum, kJobOutZ, kJobOut, kJobPick };
+enum : int { kSelCount = 0, kSelCut, kSelDraw };
+
+struct Visit {
+    int src, n;       // kSrcCands: n candidates in L.a.c
+    int lo, hi;       // kSrcRow: elements [lo, hi)
+    int job, sel;
+    uint32_t lo_k, hi_k;
+    int sh;           // kJobHist: keys in [lo_k, hi_k], bins of 2^sh keys
+    float kth, thr, m, md;
+    float* prow;
+    float* qrow;
+    float inv;
+    // per-thread results
+    float f0, f1;
+    int i0, i1;
+    unsigned long long u0, u1;
+    double d0;
+};
+
+__device__ __forceinline__ void consume(Visit& V, Lds& L, float q, int j, bool drawable) {
+    switch (V.job) {
+    case kJobStats:  // f0: max; f1: max drawable (i0: its first index); i1: finite count
+        V.f0 = fmaxf(V.f0, q);
+        if (q > -INFINITY) ++V.i1;
+        if (drawable && (q > V.f1 || (q == V.f1 && j < V.i0))) {
+            V.f1 = q;
+            V.i0 = j;
         }
+        break;
+    case kJobHist: {
+        uint32_t key;
+        unsigned long long w;
+        if (V.sel == kSelCount) {
+            key = ord_key(q);
+            w = q > -INFINITY ? 1ull : 0ull;
+        } else if (V.sel == kSelCut) {
+            key = ord_key(q);
+            w = q > V.kth ? efx(q, V.m) : 0ull;
+        } else {
+            key = (uint32_t)j;
+            w = (drawable && q >= V.thr) ? efx(q, V.md) : 0ull;
+        }
+        if (w && key >= V.lo_k && key <= V.hi_k) atomicAdd(&L.h.w[(key - V.lo_k) >> V.sh], w);
+        break;
+    }
+    case kJobSums:  // u0: mass above kth; u1: all mass (relative to m)
+        if (q > -INFINITY) {
+            const unsigned long long e = efx(q, V.m);
+            if (q > V.kth) V.u0 += e;
+            V.u1 += e;
+        }
+        break;
+    case kJobSurvMax:
+        if (drawable && q >= V.thr && q > -INFINITY) V.f0 = fmaxf(V.f0, q);
+        break;
+    case kJobSurvSum:
+        if (drawable && q >= V.thr) V.u0 += efx(q, V.md);
+        break;
+    case kJobOutZ:
+        if (drawable && q >= V.thr && q > -INFINITY) V.d0 += (double)exp_acc(q - V.md);
+        break;
+    case kJobOut: {
+        const bool keep = drawable && q >= V.thr;
+        if (V.prow) V.prow[j] = keep ? q : -INFINITY;
+        if (V.qrow)
+            V.qrow[j] = !(V.md > -INFINITY) ? NAN : ((keep && q > -INFINITY) ? exp_acc(q - V.md) * V.inv : 0.0f);
+        break;
+    }
+    case kJobPick:  // one element per thread
+        V.d0 = (drawable && q > -INFINITY) ? (double)exp_acc(q - V.m) : 0.0;
+        V.i0 = j;
+        break;
+    }
+}
+
+// Every thread calls visit.
+__device__ __forceinline__ void visit(Visit& V, const DevGroup& G, const Row& R, Lds& L) {
+    if (V.src == kSrcCands) {
+        for (int i = threadIdx.x; i < V.n; i += kThreads) {
+            const uint32_t id = L.a.c.id[i];
+            consume(V, L, L.a.c.q[i], (int)(id & ~kSelOnlyBit), !(id & kSelOnlyBit));
+        }
+        return;
+    }
+    const int chunk = kTileMax - 64;
+    for (int c0 = V.lo; c0 < V.hi; c0 += chunk) {
+        const int c1 = min(V.hi, c0 + chunk);
+        __syncthreads();
+        if (R.pen) build_counts(G, R, c0, c1 - c0, c0, c1, false, -1, L);
         build_keep(G, R.row, c0, c1 - c0, c0, c1, L);
         __syncthreads();
         for (int j = c0 + (int)threadIdx.x; j < c1; j += kThreads) {
-            const float x = load_elem<ES>(G, R.row, j);
+            const float x = load_logit(G, R.row, j);
             const int n = R.pen ? count_at(L, j - c0) : 0;
             const int o = j - ((c0 >> 5) << 5);
             const bool allowed = (L.keep[o >> 5] >> (o & 31)) & 1u;
             const float q = elem_q(R, G, x, n, allowed, j);
-            const bool drawable = !(R.eos_rule == kEosSelOnly && j == G.eos);
-            f(q, j, drawable);
+            consume(V, L, q, j, !(R.eos_rule == kEosSelOnly && j == G.eos));
         }
     }
     __syncthreads();
 }
 
-// ------------------------------------------------------------------ the finaliser
+// Scans keys in [klo, khi] in descending or ascending order and finds the first key at which the cumulative
+// weight (the selection `sel` of the visited set, plus an optional virtual element vkey of weight vw) reaches T
+// (T >= 1).  Each round histograms the keys of the current range into bins of a power-of-two width (at most kBins
+// of them), finds the bin that reaches T and narrows the range to it, until the range is one key.  False when the
+// total weight is below T; otherwise the key and the weight of every key strictly before it in scan order.
+// Weights are integers, so the result does not depend on the order of the LDS additions.
+__device__ __forceinline__ bool range_find(Visit& V, int sel, bool desc, unsigned long long T, uint32_t klo,
+                                           uint32_t khi, uint32_t vkey, unsigned long long vw, const DevGroup& G,
+                                           const Row& R, Lds& L, uint32_t& key_out, unsigned long long& before_out) {
+    Hist& h = L.h;
+    unsigned long long acc = 0;
+    for (;;) {
+        const uint64_t span = (uint64_t)khi - klo + 1;
+        int sh = 0;
+        while ((span >> sh) > (uint64_t)kBins) ++sh;
+        const int nb = (int)((span + ((1ull << sh) - 1)) >> sh);
+        for (int b = threadIdx.x; b < nb; b += kThreads) h.w[b] = 0ull;
+        __syncthreads();
+        V.job = kJobHist;
+        V.sel = sel;
+        V.lo_k = klo;
+        V.hi_k = khi;
+        V.sh = sh;
+        visit(V, G, R, L);
+        if (threadIdx.x == 0 && vw && vkey >= klo && vkey <= khi) atomicAdd(&h.w[(vkey - klo) >> sh], vw);
+        __syncthreads();
+        const int s0 = 2 * (int)threadIdx.x, s1 = s0 + 1;
+        const int b0 = desc ? nb - 1 - s0 : s0, b1 = desc ? nb - 1 - s1 : s1;
+        const unsigned long long v0 = s0 < nb ? h.w[b0] : 0ull, v1 = s1 < nb ? h.w[b1] : 0ull;
+        unsigned long long tot;
+        const unsigned long long ex = block_excl_scan(v0 + v1, tot, h.scan);
+        if (tot < T) return false;
+        if (s0 < nb && ex < T && T <= ex + v0) {
+            h.sel = b0;
+            h.before = ex;
+        } else if (s1 < nb && ex + v0 < T && T <= ex + v0 + v1) {
+            h.sel = b1;
+            h.before = ex + v0;
+        }
+        __syncthreads();
+        const int b = h.sel;
+        const unsigned long long bf = h.before;
+        T -= bf;
+        acc += bf;
+        const uint64_t a = (uint64_t)klo + ((uint64_t)b << sh);
+        klo = (uint32_t)a;
+        khi = (uint32_t)std::min<uint64_t>((uint64_t)khi, a + (1ull << sh) - 1);
+        if (sh == 0) break;
+    }
+    key_out = klo;
+    before_out = acc;
+    return true;
+}
 
 struct Outcome {
     int64_t token;
@@ -897,28 +1104,22 @@ struct Outcome {
     float mdraw;  // reference of the survivors' masses
 };
 
-// The top-k / top-p selection and the draw over a set of elements given as a source (candidates in LDS or the
-// streamed row).  m_sel: max over everything ranked; zfull_fx: the whole-vocabulary normaliser in fixed point
-// relative to m_sel (HF order or no top-k); n_fin: finite elements in the source.  Returns false when a check on
-// the candidates fails (the caller then streams).
-template <class Src>
-__device__ __forceinline__ bool select_and_draw(const DevGroup& G, const Row& R, Lds& L, Src&& src, float m_sel, double zfull_fx,
-                                int n_fin, float gate, bool all_gate_inf, bool from_cands, Outcome& out) {
+// The top-k / top-p selection (engine/talker_sampler.py:95-133) and the draw (:161-172) over a visited set.
+// m_sel: max over everything ranked; zfull_fx: the whole-vocabulary normaliser in fixed point relative to m_sel
+// (HF order, or no top-k); n_fin: finite elements in the set; [klo, khi]: key range of its values.  From the
+// candidates, every check that they hold what the selection needs is made (gate: every element >= gate is a
+// candidate); false when one fails (the caller then streams the row).
+__device__ __forceinline__ bool select_draw(const DevGroup& G, const Row& R, Lds& L, Visit& V, float m_sel,
+                                            double zfull_fx, int n_fin, float gate, bool all_gate_inf,
+                                            bool from_cands, uint32_t klo, uint32_t khi, Outcome& out) {
     const bool topk = R.kk < R.V;
     float kth = -INFINITY;
     unsigned long long cnt_gt = (unsigned long long)n_fin;
     uint32_t kkey = 0u;
+    unsigned long long bf;
     if (topk) {
         if ((unsigned long long)R.kk <= (unsigned long long)n_fin) {
-            unsigned long long bf;
-            radix_find<true>(
-                [&](auto&& f) {
-                    src([&](float q, uint32_t id) {
-                        (void)id;
-                        if (q > -INFINITY) f(ord_key(q), 1ull);
-                    });
-                },
-                (unsigned long long)R.kk, 32, L.h, kkey, bf);
+            range_find(V, kSelCount, true, (unsigned long long)R.kk, klo, khi, 0u, 0ull, G, R, L, kkey, bf);
             kth = key_float(kkey);
             cnt_gt = bf;
             if (from_cands && !(kth >= gate)) return false;
@@ -928,33 +1129,25 @@ __device__ __forceinline__ bool select_and_draw(const DevGroup& G, const Row& R,
     }
     float thr = kth;
     if (R.p_active) {
+        V.m = m_sel;
+        V.kth = kth;
         const unsigned long long ekth = efx(kth, m_sel);
         const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
         double zn;
         if (topk && !R.hf) {
-            unsigned long long part = 0ull;
-            src([&](float q, uint32_t id) {
-                (void)id;
-                if (q > kth) part += efx(q, m_sel);
-            });
-            zn = (double)(block_sum_u(part, L.red) + vw);
+            V.job = kJobSums;
+            V.u0 = V.u1 = 0ull;
+            visit(V, G, R, L);
+            zn = (double)(block_sum_u(V.u0, L.red) + vw);
         } else {
             zn = zfull_fx;
         }
         const double pt = ceil((double)R.top_p * zn);
         const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
         uint32_t ckey = 0u;
-        unsigned long long bf;
         const uint32_t kthkey = ord_key(kth);
-        const bool found = radix_find<true>(
-            [&](auto&& f) {
-                src([&](float q, uint32_t id) {
-                    (void)id;
-                    if (q > kth) f(ord_key(q), efx(q, m_sel));
-                });
-                if (threadIdx.x == 0 && vw) f(kthkey, vw);
-            },
-            T, 32, L.h, ckey, bf);
+        const bool found = range_find(V, kSelCut, true, T, (kth > -INFINITY) ? max(klo, kthkey) : klo, khi, kthkey, vw,
+                                      G, R, L, ckey, bf);
         float thr_p;
         if (found) {
             thr_p = key_float(ckey);
@@ -969,14 +1162,7 @@ __device__ __forceinline__ bool select_and_draw(const DevGroup& G, const Row& R,
             if ((unsigned long long)R.min_keep_eff > (unsigned long long)n_fin) {
                 vmk = -INFINITY;
             } else {
-                radix_find<true>(
-                    [&](auto&& f) {
-                        src([&](float q, uint32_t id) {
-                            (void)id;
-                            if (q > -INFINITY) f(ord_key(q), 1ull);
-                        });
-                    },
-                    (unsigned long long)R.min_keep_eff, 32, L.h, mk, bf);
+                range_find(V, kSelCount, true, (unsigned long long)R.min_keep_eff, klo, khi, 0u, 0ull, G, R, L, mk, bf);
                 vmk = key_float(mk);
             }
             if (from_cands && !(vmk >= gate)) return false;
@@ -985,63 +1171,52 @@ __device__ __forceinline__ bool select_and_draw(const DevGroup& G, const Row& R,
         if (topk) thr = fmaxf(thr, kth);
     }
     // survivors: drawable, finite, q >= thr
-    float md = -INFINITY;
-    src([&](float q, uint32_t id) {
-        if (!(id & kSelOnlyBit) && q >= thr && q > -INFINITY) md = fmaxf(md, q);
-    });
-    md = block_max_f(md, L.red);
+    V.job = kJobSurvMax;
+    V.thr = thr;
+    V.f0 = -INFINITY;
+    visit(V, G, R, L);
+    const float md = block_max_f(V.f0, L.red);
     out.thr = thr;
     out.mdraw = md;
     out.token = R.V - 1;
     if (!(md > -INFINITY)) return true;
-    unsigned long long zs = 0ull;
-    src([&](float q, uint32_t id) {
-        if (!(id & kSelOnlyBit) && q >= thr) zs += efx(q, md);
-    });
-    zs = block_sum_u(zs, L.red);
+    V.job = kJobSurvSum;
+    V.md = md;
+    V.u0 = 0ull;
+    visit(V, G, R, L);
+    const unsigned long long zs = block_sum_u(V.u0, L.red);
     const float u = row_uniform(G, R);
-    const double t = floor((double)u * (double)zs);
-    const unsigned long long T = (unsigned long long)t + 1ull;
+    const unsigned long long T = (unsigned long long)floor((double)u * (double)zs) + 1ull;
     uint32_t tok = 0u;
-    unsigned long long bf;
-    if (zs > 0ull && radix_find<false>(
-                         [&](auto&& f) {
-                             src([&](float q, uint32_t id) {
-                                 if (!(id & kSelOnlyBit) && q >= thr) f(id & ~kSelOnlyBit, efx(q, md));
-                             });
-                         },
-                         T, 21, L.h, tok, bf))
+    if (zs > 0ull && range_find(V, kSelDraw, false, T, 0u, (uint32_t)(R.V - 1), 0u, 0ull, G, R, L, tok, bf))
         out.token = (int64_t)tok;
     return true;
 }
 
-template <int ES>
+// Every element streamed: the reference path for any row.
 __device__ __forceinline__ void fin_stream(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
-    // pass 1: maxima, first argmax of the drawable elements, finite count
-    float m_sel = -INFINITY, m_draw = -INFINITY;
-    int arg = INT_MAX, nfin = 0;
-    stream_visit<ES>(G, R, L, 0, R.V, [&](float q, int j, bool drawable) {
-        m_sel = fmaxf(m_sel, q);
-        if (q > -INFINITY) ++nfin;
-        if (drawable && q > m_draw) {
-            m_draw = q;
-            arg = j;
-        }
-    });
+    Visit V;
+    V.src = kSrcRow;
+    V.n = 0;
+    V.lo = 0;
+    V.hi = R.V;
+    V.job = kJobStats;
+    V.f0 = V.f1 = -INFINITY;
+    V.i0 = INT_MAX;
+    V.i1 = 0;
+    V.kth = V.thr = V.m = V.md = -INFINITY;
+    visit(V, G, R, L);
+    float m_draw = V.f1;
+    int arg = V.i0;
     block_argmax(m_draw, arg, L.red);
-    m_sel = block_max_f(m_sel, L.red);
-    nfin = block_sum_i(nfin, L.red);
+    const float m_sel = block_max_f(V.f0, L.red);
+    const int nfin = block_sum_i(V.i1, L.red);
     out.thr = -INFINITY;
     out.mdraw = m_draw;
     if (R.greedy) {
         out.token = m_draw > -INFINITY ? arg : 0;
         return;
     }
-    auto src = [&](auto&& f) {
-        stream_visit<ES>(G, R, L, 0, R.V, [&](float q, int j, bool drawable) {
-            f(q, (uint32_t)j | (drawable ? 0u : kSelOnlyBit));
-        });
-    };
     Row R2 = R;
     if (!R.filters) {
         R2.kk = R.V;
@@ -1049,14 +1224,14 @@ __device__ __forceinline__ void fin_stream(const DevGroup& G, const Row& R, Lds&
     }
     double zfull = 0.0;
     if (R2.p_active && (R2.hf || R2.kk >= R2.V)) {
-        unsigned long long z = 0ull;
-        src([&](float q, uint32_t id) {
-            (void)id;
-            z += efx(q, m_sel);
-        });
-        zfull = (double)block_sum_u(z, L.red);
+        V.job = kJobSums;
+        V.m = m_sel;
+        V.kth = INFINITY;
+        V.u0 = V.u1 = 0ull;
+        visit(V, G, R, L);
+        zfull = (double)block_sum_u(V.u1, L.red);
     }
-    select_and_draw(G, R2, L, src, m_sel, zfull, nfin, -INFINITY, true, false, out);
+    select_draw(G, R2, L, V, m_sel, zfull, nfin, -INFINITY, true, false, 0u, 0xffffffffu, out);
 }
 
 // Inclusive prefix over the workgroup in thread order (doubles, fixed order).
@@ -1065,17 +1240,20 @@ __device__ __forceinline__ double block_incl_scan_d(double x, Red& r) {
     __syncthreads();
     if (lane_id() == 63) r.d[wave_id()] = incl;
     __syncthreads();
+    double p[kWaves];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) p[i] = r.d[i];
     double off = 0.0;
-    for (int i = 0; i < wave_id(); ++i) off += r.d[i];
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) off += (i < wave_id()) ? p[i] : 0.0;
     return off + incl;
 }
 
 // Candidate rows: gather every slice's candidates into LDS, select, draw.  False: stream instead.
-template <int ES>
 __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
     const int S = R.S;
     const int nseg = S * kSegs;
-    // the records: thread s reads slice s
+    // the records: thread s reads slice s; thread t reads segment counts 2t and 2t + 1
     float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
     double zz = 0.0;
     int over = 0, notinf = 0;
@@ -1089,18 +1267,17 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         over = (fl & kRecOverflow) ? 1 : 0;
         notinf = (fl & kRecGateInf) ? 0 : 1;
     }
-    const float m_sel = block_max_f(mq, L.red);
-    const float gate = block_max_f(gt, L.red);
-    if (block_max_i(over, L.red)) return false;
-    const bool all_inf = block_max_i(notinf, L.red) == 0;
-    double zs = 0.0;
-    if (R.needz) zs = block_sum_d((mr > -INFINITY && m_sel > -INFINITY) ? zz * exp((double)mr - (double)m_sel) : 0.0,
-                                  L.red);
-    // segment offsets: thread t sums segments 2t and 2t + 1
     int c0 = 0, c1 = 0;
     const int i0 = 2 * (int)threadIdx.x, i1 = i0 + 1;
     if (i0 < nseg) c0 = pub_ld(&((const SliceRec*)rec_base(G, R.row, i0 / kSegs))->ncand[i0 % kSegs]);
     if (i1 < nseg) c1 = pub_ld(&((const SliceRec*)rec_base(G, R.row, i1 / kSegs))->ncand[i1 % kSegs]);
+    const float4 m4 = block_max4(make_float4(mq, gt, over ? 1.f : 0.f, notinf ? 1.f : 0.f), L.red);
+    const float m_sel = m4.x, gate = m4.y;
+    if (m4.z > 0.f) return false;
+    const bool all_inf = !(m4.w > 0.f);
+    double zs = 0.0;
+    if (R.needz)
+        zs = block_sum_d((mr > -INFINITY && m_sel > -INFINITY) ? zz * exp((double)mr - (double)m_sel) : 0.0, L.red);
     int n;
     const int ex = block_excl_scan(c0 + c1, n, L.red.i);
     if (i0 < nseg) L.segoff[i0] = ex;
@@ -1108,6 +1285,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
     if (threadIdx.x == 0) L.segoff[nseg] = n;
     __syncthreads();
     if (n > kCapRow) return false;
+    float qmax = -INFINITY, nqmin = -INFINITY;
     for (int i = threadIdx.x; i < n; i += kThreads) {
         int lo = 0, hi = nseg;  // segment: segoff[lo] <= i < segoff[lo + 1]
         while (hi - lo > 1) {
@@ -1121,14 +1299,20 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         const unsigned long long* seg =
             (const unsigned long long*)(rec_base(G, R.row, s) + kRecCandOff) + (int64_t)sg * kCapWave;
         const unsigned long long v = pub_ld(seg + (i - L.segoff[lo]));
-        L.a.c.q[i] = __uint_as_float((uint32_t)v);
+        const float q = __uint_as_float((uint32_t)v);
+        L.a.c.q[i] = q;
         L.a.c.id[i] = (uint32_t)(v >> 32);
+        qmax = fmaxf(qmax, q);
+        nqmin = fmaxf(nqmin, -q);
     }
-    __syncthreads();
-    auto src = [&](auto&& f) {
-        for (int i = threadIdx.x; i < n; i += kThreads) f(L.a.c.q[i], L.a.c.id[i]);
-    };
-    return select_and_draw(G, R, L, src, m_sel, zs * kFx, n, gate, all_inf, true, out);
+    const float4 ext = block_max4(make_float4(qmax, nqmin, -INFINITY, -INFINITY), L.red);
+    const uint32_t klo = n ? ord_key(-ext.y) : 0u, khi = n ? ord_key(ext.x) : 0u;
+    Visit V;
+    V.src = kSrcCands;
+    V.n = n;
+    V.lo = V.hi = 0;
+    V.kth = V.thr = V.m = V.md = -INFINITY;
+    return select_draw(G, R, L, V, m_sel, zs * kFx, n, gate, all_inf, true, klo, khi, out);
 }
 
 __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
@@ -1147,9 +1331,8 @@ __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds&
 
 // Unfiltered rows: walk the slices' totals, then the chosen slice's sub-block sums, to the sub-block holding
 // u * Z, and rescan it element by element.
-template <int ES>
 __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
-    constexpr int E = Geo<ES>::E;
+    const int E = 16 / G.es;
     const int nsb = kWaves * G.R;
     const int tid = threadIdx.x;
     float mr = -INFINITY;
@@ -1192,26 +1375,30 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
     __syncthreads();
     rem = L.dscratch[2];
     const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
-    const int first = slice_geo<ES>(G, R.row, slo).first;
-    const int j0 = max(slo, first + kb * 64 * E), j1 = min(shi, first + (kb + 1) * 64 * E);
-    double e = 0.0;
-    int myj = -1;
-    stream_visit<ES>(G, R, L, j0, j1, [&](float q, int j, bool drawable) {
-        if (drawable && q > -INFINITY) e = (double)exp_acc(q - mref);
-        myj = j;
-    });
+    const int first = slice_first(G, R.row, slo);
+    Visit V;
+    V.src = kSrcRow;
+    V.n = 0;
+    V.lo = max(slo, first + kb * 64 * E);
+    V.hi = min(shi, first + (kb + 1) * 64 * E);
+    V.job = kJobPick;
+    V.m = mref;
+    V.d0 = 0.0;
+    V.i0 = -1;
+    visit(V, G, R, L);
+    const double e = V.d0;
+    const int myj = V.i0;
     incl = block_incl_scan_d(e, L.red);
     int tok = block_min_i((myj >= 0 && e > 0.0 && incl > rem) ? myj : INT_MAX, L.red);
     if (tok == INT_MAX) tok = block_max_i((myj >= 0 && e > 0.0) ? myj : -1, L.red);  // rounding: the last with mass
     if (tok >= 0) out.token = tok;
 }
 
-// Processed logits and probabilities of the whole row (parity outputs): streamed.
-template <int ES>
-__device__ __forceinline__ void write_outputs(const DevGroup& G, const Row& R, Lds& L, const Outcome& o) {
+// Processed logits and probabilities of the whole row (parity outputs), streamed.
+__device__ __forceinline__ void write_outputs(const DevGroup& G, const Row& R, Lds& L, const Outcome& o, bool forced) {
     float* prow = G.processed ? gp(G.processed) + (int64_t)R.row * G.processed_stride : nullptr;
     float* qrow = G.probs ? gp(G.probs) + (int64_t)R.row * G.probs_stride : nullptr;
-    if (R.mode == kForced) {
+    if (forced) {
         for (int j = threadIdx.x; j < R.V; j += kThreads) {
             const bool e = j == G.eos;
             if (prow) prow[j] = e ? 0.0f : -INFINITY;
@@ -1219,21 +1406,25 @@ __device__ __forceinline__ void write_outputs(const DevGroup& G, const Row& R, L
         }
         return;
     }
-    const float thr = o.thr, md = o.mdraw;
+    Visit V;
+    V.src = kSrcRow;
+    V.n = 0;
+    V.lo = 0;
+    V.hi = R.V;
+    V.thr = o.thr;
+    V.md = o.mdraw;
+    V.prow = prow;
+    V.qrow = qrow;
+    V.d0 = 0.0;
     double z = 0.0;
-    if (qrow && md > -INFINITY) {
-        stream_visit<ES>(G, R, L, 0, R.V, [&](float q, int j, bool drawable) {
-            (void)j;
-            if (drawable && q >= thr && q > -INFINITY) z += (double)exp_acc(q - md);
-        });
-        z = block_sum_d(z, L.red);
+    if (qrow && o.mdraw > -INFINITY) {
+        V.job = kJobOutZ;
+        visit(V, G, R, L);
+        z = block_sum_d(V.d0, L.red);
     }
-    const float inv = (float)(1.0 / z);
-    stream_visit<ES>(G, R, L, 0, R.V, [&](float q, int j, bool drawable) {
-        const bool keep = drawable && q >= thr;
-        if (prow) prow[j] = keep ? q : -INFINITY;
-        if (qrow) qrow[j] = !(md > -INFINITY) ? NAN : ((keep && q > -INFINITY) ? exp_acc(q - md) * inv : 0.0f);
-    });
+    V.inv = (float)(1.0 / z);
+    V.job = kJobOut;
+    visit(V, G, R, L);
 }
 
 // tokens[row]; for live rows with MIS_UPDATE_STATE: history append, steps + 1, finished |= (token == eos).
@@ -1283,37 +1474,25 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Row& R, in
     }
 }
 
-template <int ES>
-__device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L) {
+// The row's last workgroup (or slice 0 of a forced row).
+__device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L, bool forced) {
     Outcome o;
-    o.token = 0;
+    o.token = forced ? (int64_t)G.eos : 0;
     o.thr = -INFINITY;
     o.mdraw = -INFINITY;
-    int mode = L.foreign ? kStream : R.mode;
-    if (mode == kGreedy) {
-        fin_greedy(G, R, L, o);
-    } else if (mode == kFull) {
-        fin_full<ES>(G, R, L, o);
-    } else if (mode == kTopK || mode == kNucleus) {
-        if (!fin_cands<ES>(G, R, L, o)) mode = kStream;
+    if (!forced) {
+        int mode = L.foreign ? kStream : R.mode;
+        if (mode == kGreedy) {
+            fin_greedy(G, R, L, o);
+        } else if (mode == kFull) {
+            fin_full(G, R, L, o);
+        } else if (mode == kTopK || mode == kNucleus) {
+            if (!fin_cands(G, R, L, o)) mode = kStream;
+        }
+        if (mode == kStream) fin_stream(G, R, L, o);
     }
-    if (mode == kStream) fin_stream<ES>(G, R, L, o);
-    if (R.want_out) write_outputs<ES>(G, R, L, o);
+    if (R.want_out) write_outputs(G, R, L, o, forced);
     update_state(G, R, o.token);
-}
-
-__device__ __forceinline__ void forced_row(const DevGroup& G, const Row& R, Lds& L) {
-    Outcome o;
-    o.token = G.eos;
-    o.thr = -INFINITY;
-    o.mdraw = 0.f;
-    if (R.want_out) {
-        if (G.es == 2)
-            write_outputs<2>(G, R, L, o);
-        else
-            write_outputs<4>(G, R, L, o);
-    }
-    update_state(G, R, G.eos);
 }
 
 __device__ __forceinline__ bool locate(const KernelArgs& A, int& gi, int& row, int& slice) {
@@ -1340,19 +1519,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const KernelArgs args)
     int gi, row, slice;
     if (!locate(A, gi, row, slice)) return;
     const DevGroup& G = A.g[gi];
-    const Row R = make_row(G, gi, row, slice);
-    if (R.mode == kSkip) {
-        if (slice == 0 && threadIdx.x == 0 && G.tokens) gp(G.tokens)[row] = kPad;
-        return;
-    }
-    if (R.mode == kForced) {
-        if (slice == 0) forced_row(G, R, L);
-        return;
-    }
-    if (G.es == 2) {
-        if (slice_phase<2>(A, G, R, L)) finalize<2>(G, R, L);
-    } else {
-        if (slice_phase<4>(A, G, R, L)) finalize<4>(G, R, L);
+    Row R;
+    const int act = G.es == 2 ? run<2>(A, G, gi, row, slice, L, R) : run<4>(A, G, gi, row, slice, L, R);
+    if (act != kActNone) {
+        if (act == kActForced) L.foreign = 0;
+        finalize(G, R, L, act == kActForced);
     }
 }
 
@@ -1388,7 +1559,7 @@ struct Plan {
 Plan plan_group(const MisGroup& g, int rows_total) {
     const int es = g.dtype == MIS_BF16 ? 2 : 4;
     const int E = 16 / es;
-    const int rmax = kTileElems / E;
+    const int rmax = kRounds;
     auto len_of = [&](int r) { return kThreads * E * r - E; };
     Plan p;
     if ((int64_t)g.vocab * es <= 48 * 1024) {
