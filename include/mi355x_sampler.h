@@ -51,6 +51,20 @@ enum {
 
 enum { MIS_E_ARG = 1, MIS_E_WORKSPACE = 2, MIS_E_UNSUPPORTED = 3 };
 
+/* Diagnostics (no reference counterpart): bytes [MIS_WS_PATH_OFFSET, + 4 * MIS_PATH_COUNT) of the workspace hold one
+ * uint32 counter per finalisation path, incremented once per sampled row and never cleared by the library; a caller
+ * that wants per-launch figures zeroes them before the launch.  Which path a row takes never changes its result. */
+#define MIS_WS_PATH_OFFSET 64
+enum {
+    MIS_PATH_GREEDY = 0,     /* first argmax from the slices' maxima */
+    MIS_PATH_FULL = 1,       /* no filter: the slices' sub-block sums, one sub-block rescanned */
+    MIS_PATH_CANDIDATES = 2, /* top-k / top-p selection over the slices' candidates */
+    MIS_PATH_HISTOGRAM = 3,  /* top-p without top-k, bf16: the slices' value histograms, one slice rescanned */
+    MIS_PATH_STREAM = 4,     /* the whole row from its logits */
+    MIS_PATH_FORCED = 5,     /* EOS forced at max_new_tokens */
+    MIS_PATH_COUNT = 6
+};
+
 /* One group of rows that share a vocabulary size, dtype and pipeline order.
  * Per-row parameter arrays may be NULL, in which case the scalar *_value applies
  * to every row (the reference's single TalkerSampling). */

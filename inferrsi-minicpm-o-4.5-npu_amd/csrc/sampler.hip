@@ -53,9 +53,10 @@ constexpr int kSegs = kWaves + 1;                // candidate segments of a slic
 constexpr int kCapRow = 12288;                   // candidates a finaliser gathers
 constexpr int kBins = 2048;                      // radix digit: 11 bits
 constexpr int kMaxSB = kWaves * kRounds;         // (wave, round) sub-blocks of a slice
-constexpr double kFx = 35184372088832.0;         // 2^45 fixed-point units of exp(q - max)
+constexpr double kFx = 4398046511104.0;          // 2^42 fixed-point units of exp(q - max): V * 2^42 < 2^64
 constexpr int kLineBytes = 128;                  // a row's arrival word has a cache line of its own
-constexpr int64_t kHeaderBytes = 256;            // status word
+constexpr int64_t kHeaderBytes = 256;            // diagnostic counters (MIS_WS_PATH_OFFSET)
+static_assert(MIS_WS_PATH_OFFSET + 4 * MIS_PATH_COUNT <= kHeaderBytes, "workspace header");
 // Arrival words live at fixed offsets (they must read zero at every launch, whatever the previous launch's shape).
 constexpr int64_t kArriveBytes = (int64_t)kMaxRows * kLineBytes;
 constexpr int kPad = -1;
@@ -104,6 +105,7 @@ struct DevGroup {
     int32_t slice_len;  // elements per slice (the last one may be shorter)
     int32_t row_begin;  // index of the group's first row among the launch's rows
     char* recs;         // slice records: [rows][S] x kRecBytes
+    uint32_t* paths;    // rows finalised per path (MIS_PATH_*), diagnostics
 };
 
 // Whole rows are assigned to XCDs: block b runs on XCD b % 8 (the dispatcher's round-robin) as the (b / 8)-th
@@ -113,8 +115,7 @@ struct KernelArgs {
     int32_t n_groups;
     int32_t seg_row[8][kMaxGroups];
     int32_t seg_rows[8][kMaxGroups];
-    char* arrive;      // per launch row: a 64-bit arrival word, kLineBytes apart
-    uint32_t* status;  // sticky error bits (MIS_STATUS_*)
+    char* arrive;  // per launch row: a 64-bit arrival word, kLineBytes apart
 };
 
 // What a slice publishes for its row's finaliser.
@@ -125,15 +126,27 @@ struct SliceRec {
     float mref;      // reference of z and of the sub-block sums
     int32_t argmax;  // first index of mqd (greedy rows)
     int32_t flags;   // kRec*
-    int32_t pad0, pad1;
+    int32_t hist;    // 1: the nucleus histogram and the specials list are published
+    int32_t nspec;   // specials published
     double z;        // sum of exp(q - mref) (whole-vocabulary normaliser, unfiltered rows)
     int32_t ncand[kSegs];
+    int32_t pad0;
+    unsigned long long tinyfx;  // sum of exp(q) in fixed point over the tiny-magnitude lumps of the histogram
 };
 constexpr int64_t kRecHead = 256;
 static_assert(sizeof(SliceRec) <= kRecHead, "slice record");
 constexpr int64_t kRecSbOff = kRecHead;
 constexpr int64_t kRecCandOff = kRecSbOff + 8 * kMaxSB;
-constexpr int64_t kRecBytes = kRecCandOff + 8 * (kWaves * kCapWave + kCapSpecSeg);
+// Nucleus histogram of a bf16 slice: one key per bf16 value with |x| in [2^-7, 2^8) (1,920 per sign), zero, the
+// tiny magnitudes of each sign (lumps) and the huge ones (lumps); keys increase with the value.
+constexpr int kKeys = 3845;
+constexpr int kKeyZero = 1922;
+constexpr uint32_t kBfLo = 0x3C00u;  // 2^-7
+constexpr uint32_t kBfHi = 0x4380u;  // 2^8
+constexpr int kHistWords = (kKeys + 1) / 2;  // published as u16 pairs
+constexpr int64_t kRecHistOff = kRecCandOff + 8 * (kWaves * kCapWave + kCapSpecSeg);
+constexpr int64_t kRecSpecOff = kRecHistOff + 4 * ((kHistWords + 63) / 64 * 64);
+constexpr int64_t kRecBytes = kRecSpecOff + 8 * kSpecCap;
 
 struct Special {
     int32_t j;    // token id
@@ -172,6 +185,9 @@ struct Lds {
     int32_t token;
     float fscratch[4];
     double dscratch[4];
+    unsigned long long tinyfx;               // slice phase: the histogram's tiny lumps
+    unsigned long long uscratch[2];
+    unsigned long long slice_u[kMaxSlices];  // finaliser: per-slice sums
 };
 static_assert(sizeof(Lds) <= 160 * 1024, "LDS budget");
 
@@ -608,6 +624,34 @@ __device__ __forceinline__ float to_q(const Row& R, float x) {
     return ES == 2 ? div_rn(x, R.rT) : x;
 }
 
+// Histogram key of a finite bf16 value b (raw bits); -0 is zero.  Keys increase with the value.
+__device__ __forceinline__ int bf_key(uint32_t b) {
+    const uint32_t a = b & 0x7fffu;
+    if (a == 0u) return kKeyZero;
+    const bool neg = (b & 0x8000u) != 0u;
+    if (a < kBfLo) return neg ? kKeyZero - 1 : kKeyZero + 1;
+    if (a >= kBfHi) return neg ? 0 : kKeys - 1;
+    const int m = (int)(a - kBfLo);
+    return neg ? kKeyZero - 2 - m : kKeyZero + 2 + m;
+}
+
+// Keys that hold one value: every key but the lumps (0, kKeyZero - 1, kKeyZero + 1, kKeys - 1).
+__device__ __forceinline__ bool key_exact(int k) {
+    return k >= 1 && k <= kKeys - 2 && k != kKeyZero - 1 && k != kKeyZero + 1;
+}
+
+// The bf16 value of an exact key.
+__device__ __forceinline__ float key_bf(int k) {
+    uint32_t b;
+    if (k == kKeyZero)
+        b = 0u;
+    else if (k > kKeyZero)
+        b = kBfLo + (uint32_t)(k - kKeyZero - 2);
+    else
+        b = 0x8000u | (kBfLo + (uint32_t)(kKeyZero - 2 - k));
+    return __uint_as_float(b << 16);
+}
+
 // A value g such that at least c lanes of the wave have lmax >= g, by bisection between the wave's smallest and
 // largest finite lane maxima (-inf when fewer than c lanes hold a finite value).  Any element among the wave's c
 // largest is >= g: c lane maxima are >= g, and an element below g is exceeded by all of them.
@@ -855,6 +899,14 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     int cnt = 0, flags = 0;
     double zacc = 0.0;
     const float mref = mq;
+    // bf16 top-p rows without top-k also publish the count of every value (the nucleus histogram) and their
+    // specials, which settle a nucleus wider than the candidates
+    const bool hist = ES == 2 && R.mode == kNucleus && R.T >= 0.015625f;
+    if (hist) {
+        uint32_t* hk = (uint32_t*)L.h.w;
+        for (int i = tid; i < 2 * kBins; i += kThreads) hk[i] = 0u;
+        if (tid == 0) L.tinyfx = 0ull;
+    }
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
         if (r >= RR) continue;
@@ -881,7 +933,40 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         L.red.d[w] = zacc;
         if (flags) atomicOr(&L.flags, flags);
     }
+    if constexpr (ES == 2) {
+        if (hist) {
+            // counts by value key; the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
+            uint32_t* hk = (uint32_t*)L.h.w;
+            unsigned long long tf = 0ull;
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (r >= RR) continue;
+                const uint32_t wv[4] = {t[r].x, t[r].y, t[r].z, t[r].w};
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
+                    if (b != 0xff80u) {
+                        const int k = bf_key(b);
+                        atomicAdd(&hk[k], 1u);
+                        if (k == kKeyZero - 1 || k == kKeyZero + 1)
+                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, __uint_as_float(b << 16))) * kFx);
+                    }
+                }
+            }
+            tf = wave_reduce(tf, [](unsigned long long a, unsigned long long b) { return a + b; });
+            if (l == 0 && tf) atomicAdd(&L.tinyfx, tf);
+        }
+    }
     __syncthreads();
+    if (hist) {
+        const uint32_t* hk = (const uint32_t*)L.h.w;
+        uint32_t* hg = (uint32_t*)((char*)rec + kRecHistOff);
+        for (int i = tid; i < kHistWords; i += kThreads) hg[i] = hk[2 * i] | (hk[2 * i + 1] << 16);
+        unsigned long long* sg = (unsigned long long*)((char*)rec + kRecSpecOff);
+        for (int i = tid; i < ns; i += kThreads)
+            sg[i] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
+                    __float_as_uint(L.spec[i].q);
+    }
     float gs = -INFINITY;
     double z = 0.0;
 #pragma unroll
@@ -914,6 +999,9 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             rec->mref = mref;
             rec->z = z + sz;
             rec->flags = L.flags | sflags | (gs > -INFINITY ? 0 : kRecGateInf);
+            rec->hist = hist ? 1 : 0;
+            rec->nspec = ns;
+            rec->tinyfx = L.tinyfx;
         }
     }
     if (tid < kWaves) rec->ncand[tid] = L.segoff[tid];
@@ -939,12 +1027,19 @@ __device__ __forceinline__ int slice_first(const DevGroup& G, int row, int lo) {
     return lo - (int)((lo_addr & 15) / G.es);
 }
 
-enum : int { kSrcCands = 0, kSrcRow = 1 };
+enum : int { kSrcCands = 0, kSrcRow = 1, kSrcHistSlice = 2 };
 enum : int { kJobStats = 0, kJobHist, kJobSums, kJobSurvMax, kJobSurvSum, kJobOutZ, kJobOut, kJobPick };
 enum : int { kSelCount = 0, kSelCut, kSelDraw };
 
 struct Visit {
-    int src, n;       // kSrcCands: n candidates in L.a.c
+    int src, n;       // kSrcCands: n candidates in L.a.c (weighted: the id field holds a multiplicity)
+    bool weighted;
+    // kSrcHistSlice: elements [lo, hi) of the row weigh lut[key] (lumps: their own mass when lump_surv), special
+    // positions (L.keep bits from lo rounded down to 32) are skipped, and the nsp specials at spl weigh their own
+    const unsigned long long* lut;
+    const unsigned long long* spl;
+    int nsp;
+    bool lump_surv;
     int lo, hi;       // kSrcRow: elements [lo, hi)
     int job, sel;
     uint32_t lo_k, hi_k;
@@ -960,11 +1055,12 @@ struct Visit {
     double d0;
 };
 
-__device__ __forceinline__ void consume(Visit& V, Lds& L, float q, int j, bool drawable) {
+__device__ __forceinline__ void consume(Visit& V, Lds& L, float q, int j, bool drawable,
+                                        unsigned long long mult = 1ull) {
     switch (V.job) {
     case kJobStats:  // f0: max; f1: max drawable (i0: its first index); i1: finite count
         V.f0 = fmaxf(V.f0, q);
-        if (q > -INFINITY) ++V.i1;
+        if (q > -INFINITY) V.i1 += (int)mult;
         if (drawable && (q > V.f1 || (q == V.f1 && j < V.i0))) {
             V.f1 = q;
             V.i0 = j;
@@ -975,10 +1071,10 @@ __device__ __forceinline__ void consume(Visit& V, Lds& L, float q, int j, bool d
         unsigned long long w;
         if (V.sel == kSelCount) {
             key = ord_key(q);
-            w = q > -INFINITY ? 1ull : 0ull;
+            w = q > -INFINITY ? mult : 0ull;
         } else if (V.sel == kSelCut) {
             key = ord_key(q);
-            w = q > V.kth ? efx(q, V.m) : 0ull;
+            w = q > V.kth ? mult * efx(q, V.m) : 0ull;
         } else {
             key = (uint32_t)j;
             w = (drawable && q >= V.thr) ? efx(q, V.md) : 0ull;
@@ -988,7 +1084,7 @@ __device__ __forceinline__ void consume(Visit& V, Lds& L, float q, int j, bool d
     }
     case kJobSums:  // u0: mass above kth; u1: all mass (relative to m)
         if (q > -INFINITY) {
-            const unsigned long long e = efx(q, V.m);
+            const unsigned long long e = mult * efx(q, V.m);
             if (q > V.kth) V.u0 += e;
             V.u1 += e;
         }
@@ -997,7 +1093,7 @@ __device__ __forceinline__ void consume(Visit& V, Lds& L, float q, int j, bool d
         if (drawable && q >= V.thr && q > -INFINITY) V.f0 = fmaxf(V.f0, q);
         break;
     case kJobSurvSum:
-        if (drawable && q >= V.thr) V.u0 += efx(q, V.md);
+        if (drawable && q >= V.thr) V.u0 += mult * efx(q, V.md);
         break;
     case kJobOutZ:
         if (drawable && q >= V.thr && q > -INFINITY) V.d0 += (double)exp_acc(q - V.md);
@@ -1021,7 +1117,44 @@ __device__ __forceinline__ void visit(Visit& V, const DevGroup& G, const Row& R,
     if (V.src == kSrcCands) {
         for (int i = threadIdx.x; i < V.n; i += kThreads) {
             const uint32_t id = L.a.c.id[i];
-            consume(V, L, L.a.c.q[i], (int)(id & ~kSelOnlyBit), !(id & kSelOnlyBit));
+            const uint32_t v = id & ~kSelOnlyBit;
+            consume(V, L, L.a.c.q[i], (int)v, !(id & kSelOnlyBit), V.weighted ? (unsigned long long)v : 1ull);
+        }
+        return;
+    }
+    if (V.src == kSrcHistSlice) {  // the draw's histogram rounds over one slice (keys are token ids)
+        const int lo = max(V.lo, (int)V.lo_k), hi = min(V.hi, (int)V.hi_k + 1);
+        const Geo<2> g = slice_geo<2>(G, R.row, lo);
+        const uint32_t* mrow = G.allowed ? gp(G.allowed) + (int64_t)R.row * G.allowed_stride : nullptr;
+        const int jb = (V.lo >> 5) << 5;
+        const int nch = hi > lo ? (hi - g.first + 7) / 8 : 0;
+        for (int c = threadIdx.x; c < nch; c += kThreads) {
+            const uint4 v = load_chunk<2>(g, c, hi);
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            const int j0 = g.first + 8 * c;
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const int j = j0 + h;
+                const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
+                if (j < lo || j >= hi || b == 0xff80u) continue;
+                if (mrow && !((mrow[j >> 5] >> (j & 31)) & 1u)) continue;
+                if ((L.keep[(j - jb) >> 5] >> ((j - jb) & 31)) & 1u) continue;  // a special
+                if (R.eos_rule != kEosNormal && j == G.eos) continue;
+                const int k = bf_key(b);
+                unsigned long long w = V.lut[k];
+                if (V.lump_surv && (k == kKeyZero - 1 || k == kKeyZero + 1))
+                    w = efx(to_q<2>(R, __uint_as_float(b << 16)), V.md);
+                if (w) atomicAdd(&L.h.w[((uint32_t)j - V.lo_k) >> V.sh], w);
+            }
+        }
+        for (int i = threadIdx.x; i < V.nsp; i += kThreads) {
+            const unsigned long long e = pub_ld(V.spl + i);
+            const uint32_t id = (uint32_t)(e >> 32);
+            const float q = __uint_as_float((uint32_t)e);
+            const uint32_t j = id & ~kSelOnlyBit;
+            if ((id & kSelOnlyBit) || !(q >= V.thr) || j < V.lo_k || j > V.hi_k) continue;
+            const unsigned long long w = efx(q, V.md);
+            if (w) atomicAdd(&L.h.w[(j - V.lo_k) >> V.sh], w);
         }
         return;
     }
@@ -1196,6 +1329,7 @@ __device__ __forceinline__ bool select_draw(const DevGroup& G, const Row& R, Lds
 // Every element streamed: the reference path for any row.
 __device__ __forceinline__ void fin_stream(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
     Visit V;
+    V.weighted = false;
     V.src = kSrcRow;
     V.n = 0;
     V.lo = 0;
@@ -1308,11 +1442,255 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
     const float4 ext = block_max4(make_float4(qmax, nqmin, -INFINITY, -INFINITY), L.red);
     const uint32_t klo = n ? ord_key(-ext.y) : 0u, khi = n ? ord_key(ext.x) : 0u;
     Visit V;
+    V.weighted = false;
     V.src = kSrcCands;
     V.n = n;
     V.lo = V.hi = 0;
     V.kth = V.thr = V.m = V.md = -INFINITY;
     return select_draw(G, R, L, V, m_sel, zs * kFx, n, gate, all_inf, true, klo, khi, out);
+}
+
+// Room in the finaliser's LDS list for the lanes where pred holds (wave-aggregated); -1 where it does not.
+__device__ __forceinline__ int lds_reserve(bool pred, int* counter) {
+    const uint64_t b = ballot(pred);
+    if (b == 0ull) return -1;
+    const int leader = __ffsll((long long)b) - 1;
+    int base = 0;
+    if (lane_id() == leader) base = atomicAdd(counter, __popcll(b));
+    base = __builtin_amdgcn_readlane(base, leader);
+    return pred ? base + (int)rank_below(b) : -1;
+}
+
+// Top-p rows without top-k on bf16 logits whose nucleus the candidates do not hold.  The cut comes from every
+// slice's value counts and specials, as a weighted selection (one entry per value present with its count, one per
+// special; the tiny-magnitude lumps as one element at 0 with their summed mass, which may not be where the cut
+// falls).  Each slice's survivor mass follows from its counts; the draw streams the one slice that holds it.
+// False: the row is streamed instead.
+__device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
+    const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
+    const float u = tid == 0 ? row_uniform(G, R) : 0.f;
+    if (w == 0) {  // lane s reads slice s's record
+        float mq = -INFINITY, mqd = -INFINITY, mr = -INFINITY;
+        double zz = 0.0;
+        int bad = 0, nsp = 0;
+        unsigned long long tf = 0ull;
+        if (l < S) {
+            const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
+            mq = pub_ld(&rec->mq);
+            mqd = pub_ld(&rec->mqd);
+            mr = pub_ld(&rec->mref);
+            zz = pub_ld(&rec->z);
+            bad = (!pub_ld(&rec->hist) || (pub_ld(&rec->flags) & kRecOverflow)) ? 1 : 0;
+            nsp = pub_ld(&rec->nspec);
+            tf = pub_ld(&rec->tinyfx);
+        }
+        const float m = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
+        const float md = wave_reduce(mqd, [](float a, float b) { return fmaxf(a, b); });
+        const int anybad = wave_reduce(bad, [](int a, int b) { return max(a, b); });
+        const double zn = wave_reduce((mr > -INFINITY && m > -INFINITY) ? zz * exp((double)mr - (double)m) : 0.0,
+                                      [](double a, double b) { return a + b; });
+        const int incl = wave_incl_scan(nsp);
+        if (l < S) {
+            L.segoff[l] = incl - nsp;
+            L.slice_u[l] = tf;
+        }
+        if (l == 0) {
+            L.segoff[S] = __builtin_amdgcn_readlane(incl, 63);
+            L.fscratch[0] = m;
+            L.fscratch[1] = md;
+            L.dscratch[0] = zn;
+            L.token = anybad;
+            L.nspec = 0;
+        }
+    }
+    __syncthreads();
+    if (L.token) return false;
+    const float m = L.fscratch[0], mdraw = L.fscratch[1];
+    const double zn = L.dscratch[0] * kFx;
+    const int ntot = L.segoff[S];
+    out.thr = -INFINITY;
+    out.mdraw = -INFINITY;
+    out.token = R.V - 1;
+    if (!(m > -INFINITY)) return true;
+    // every slice's counts, merged
+    uint32_t* cnt = (uint32_t*)L.h.w;
+    for (int i = tid; i < kHistWords; i += kThreads) {
+        uint32_t a = 0u, b = 0u;
+        for (int s = 0; s < S; ++s) {
+            const uint32_t v = pub_ld((const uint32_t*)(rec_base(G, R.row, s) + kRecHistOff) + i);
+            a += v & 0xffffu;
+            b += v >> 16;
+        }
+        cnt[2 * i] = a;
+        cnt[2 * i + 1] = b;
+    }
+    __syncthreads();
+    const uint32_t nlump = cnt[kKeyZero - 1] + cnt[kKeyZero + 1];
+    if (cnt[kKeys - 1] != 0u) return false;  // values of 256 and above are not resolved here
+    // the weighted list: values present (exact keys), then every special (the censored EOS ranks but is not drawn)
+    float qmax = -INFINITY, nqmin = -INFINITY;
+    for (int k0 = 0; k0 < kKeys; k0 += kThreads) {
+        const int k = k0 + tid;
+        const uint32_t c = (k < kKeys && key_exact(k)) ? cnt[k] : 0u;
+        const int slot = lds_reserve(c != 0u, &L.nspec);
+        if (slot >= 0 && slot < kCapRow) {
+            const float q = to_q<2>(R, key_bf(k));
+            L.a.c.q[slot] = q;
+            L.a.c.id[slot] = c;
+            qmax = fmaxf(qmax, q);
+            nqmin = fmaxf(nqmin, -q);
+        }
+    }
+    __syncthreads();
+    const int n0 = L.nspec;
+    const int n = n0 + ntot;
+    if (n > kCapRow) return false;
+    for (int i = tid; i < ntot; i += kThreads) {
+        int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (L.segoff[mid] <= i)
+                lo = mid;
+            else
+                hi = mid;
+        }
+        const unsigned long long e =
+            pub_ld((const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) + (i - L.segoff[lo]));
+        const float q = __uint_as_float((uint32_t)e);
+        L.a.c.q[n0 + i] = q;
+        L.a.c.id[n0 + i] = 1u | ((uint32_t)(e >> 32) & kSelOnlyBit);
+        if (q > -INFINITY) {
+            qmax = fmaxf(qmax, q);
+            nqmin = fmaxf(nqmin, -q);
+        }
+    }
+    unsigned long long tiny0 = 0ull;
+    for (int s = 0; s < S; ++s) tiny0 += L.slice_u[s];
+    const float4 ext = block_max4(make_float4(qmax, nqmin, -INFINITY, -INFINITY), L.red);
+    const uint32_t k0key = ord_key(0.0f);
+    uint32_t klo = n ? ord_key(-ext.y) : k0key, khi = n ? ord_key(ext.x) : k0key;
+    if (nlump) {
+        klo = min(klo, k0key);
+        khi = max(khi, k0key);
+    }
+    // the cut (engine/talker_sampler.py:87-92 semantics through the fixed-point masses of select_draw)
+    Visit V;
+    V.src = kSrcCands;
+    V.n = n;
+    V.weighted = true;
+    V.lo = V.hi = 0;
+    V.kth = V.thr = V.md = -INFINITY;
+    V.m = m;
+    const float q_tlo = to_q<2>(R, -0.0078125f), q_thi = to_q<2>(R, 0.0078125f);
+    const unsigned long long lump_m = nlump ? (unsigned long long)((double)tiny0 * exp(-(double)m)) : 0ull;
+    const double pt = ceil((double)R.top_p * zn);
+    const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+    uint32_t ckey = 0u;
+    unsigned long long bf;
+    if (!range_find(V, kSelCut, true, T, klo, khi, k0key, lump_m, G, R, L, ckey, bf)) return false;
+    const float thr_p = key_float(ckey);
+    if (nlump && thr_p > q_tlo && thr_p < q_thi) return false;
+    float vmk = m;
+    if (R.min_keep_eff >= 2) {
+        uint32_t mk = 0u;
+        if (range_find(V, kSelCount, true, (unsigned long long)R.min_keep_eff, klo, khi, k0key, nlump, G, R, L, mk,
+                       bf)) {
+            vmk = key_float(mk);
+            if (nlump && vmk > q_tlo && vmk < q_thi) return false;
+        } else {
+            vmk = -INFINITY;
+        }
+    }
+    const float thr = fminf(thr_p, vmk);
+    const float md = mdraw >= thr ? mdraw : -INFINITY;
+    out.thr = thr;
+    out.mdraw = md;
+    if (!(md > -INFINITY)) return true;
+    // survivor masses by key (relative to md), then per slice: counts, specials, the lumps when they survive
+    unsigned long long* lut = (unsigned long long*)L.a.c.q;
+    for (int k = tid; k <= kKeys; k += kThreads) {
+        unsigned long long e = 0ull;
+        if (k < kKeys && key_exact(k)) {
+            const float q = to_q<2>(R, key_bf(k));
+            if (q >= thr) e = efx(q, md);
+        }
+        lut[k] = e;
+    }
+    const bool lump_surv = nlump && thr <= q_tlo;
+    __syncthreads();
+    for (int s = w; s < S; s += kWaves) {
+        const char* rb = rec_base(G, R.row, s);
+        const uint32_t* hg = (const uint32_t*)(rb + kRecHistOff);
+        unsigned long long acc = 0ull;
+        for (int i = l; i < kHistWords; i += 64) {
+            const uint32_t v = pub_ld(hg + i);
+            acc += (unsigned long long)(v & 0xffffu) * lut[2 * i] + (unsigned long long)(v >> 16) * lut[2 * i + 1];
+        }
+        const unsigned long long* sg = (const unsigned long long*)(rb + kRecSpecOff);
+        const int ns = L.segoff[s + 1] - L.segoff[s];
+        for (int i = l; i < ns; i += 64) {
+            const unsigned long long e = pub_ld(sg + i);
+            const float q = __uint_as_float((uint32_t)e);
+            if (!((uint32_t)(e >> 32) & kSelOnlyBit) && q >= thr) acc += efx(q, md);
+        }
+        acc = wave_reduce(acc, [](unsigned long long a, unsigned long long b) { return a + b; });
+        if (lump_surv) acc += (unsigned long long)((double)L.slice_u[s] * exp(-(double)md));
+        if (l == 0) L.sbfx[s] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long zs = 0ull;
+        for (int s = 0; s < S; ++s) zs += L.sbfx[s];
+        int ss = -1;
+        unsigned long long rem = 0ull;
+        if (zs > 0ull) {
+            const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
+            unsigned long long c = 0ull;
+            for (int s = 0; s < S; ++s) {
+                const unsigned long long v = L.sbfx[s];
+                if (v && c + v >= T2) {
+                    ss = s;
+                    rem = T2 - c;
+                    break;
+                }
+                c += v;
+            }
+        }
+        L.is_last = ss;
+        L.uscratch[0] = rem;
+    }
+    __syncthreads();
+    const int ss = L.is_last;
+    const unsigned long long rem = L.uscratch[0];
+    if (ss < 0) return true;
+    // the draw inside slice ss: its specials as L.keep bits (skipped in the stream, weighed from their list)
+    const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
+    const int jb = (slo >> 5) << 5;
+    const int nkw = (shi - jb + 31) / 32;
+    for (int k = tid; k < nkw; k += kThreads) L.keep[k] = 0u;
+    __syncthreads();
+    const unsigned long long* spl = (const unsigned long long*)(rec_base(G, R.row, ss) + kRecSpecOff);
+    const int nsp = L.segoff[ss + 1] - L.segoff[ss];
+    for (int i = tid; i < nsp; i += kThreads) {
+        const int j = (int)((uint32_t)(pub_ld(spl + i) >> 32) & ~kSelOnlyBit);
+        atomicOr(&L.keep[(j - jb) >> 5], 1u << ((j - jb) & 31));
+    }
+    __syncthreads();
+    V.src = kSrcHistSlice;
+    V.weighted = false;
+    V.lo = slo;
+    V.hi = shi;
+    V.lut = lut;
+    V.spl = spl;
+    V.nsp = nsp;
+    V.lump_surv = lump_surv;
+    V.thr = thr;
+    V.md = md;
+    uint32_t tok = 0u;
+    if (!range_find(V, kSelDraw, false, rem, (uint32_t)slo, (uint32_t)(shi - 1), 0u, 0ull, G, R, L, tok, bf))
+        return false;
+    out.token = (int64_t)tok;
+    return true;
 }
 
 __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
@@ -1377,6 +1755,7 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
     const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
     const int first = slice_first(G, R.row, slo);
     Visit V;
+    V.weighted = false;
     V.src = kSrcRow;
     V.n = 0;
     V.lo = max(slo, first + kb * 64 * E);
@@ -1407,6 +1786,7 @@ __device__ __forceinline__ void write_outputs(const DevGroup& G, const Row& R, L
         return;
     }
     Visit V;
+    V.weighted = false;
     V.src = kSrcRow;
     V.n = 0;
     V.lo = 0;
@@ -1480,17 +1860,28 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
     o.token = forced ? (int64_t)G.eos : 0;
     o.thr = -INFINITY;
     o.mdraw = -INFINITY;
+    int path = MIS_PATH_FORCED;
     if (!forced) {
         int mode = L.foreign ? kStream : R.mode;
         if (mode == kGreedy) {
             fin_greedy(G, R, L, o);
+            path = MIS_PATH_GREEDY;
         } else if (mode == kFull) {
             fin_full(G, R, L, o);
+            path = MIS_PATH_FULL;
         } else if (mode == kTopK || mode == kNucleus) {
-            if (!fin_cands(G, R, L, o)) mode = kStream;
+            path = MIS_PATH_CANDIDATES;
+            if (!fin_cands(G, R, L, o)) {
+                path = MIS_PATH_HISTOGRAM;
+                if (!(mode == kNucleus && G.es == 2 && fin_hist(G, R, L, o))) mode = kStream;
+            }
         }
-        if (mode == kStream) fin_stream(G, R, L, o);
+        if (mode == kStream) {
+            fin_stream(G, R, L, o);
+            path = MIS_PATH_STREAM;
+        }
     }
+    if (threadIdx.x == 0 && G.paths) atomicAdd(G.paths + path, 1u);
     if (R.want_out) write_outputs(G, R, L, o, forced);
     update_state(G, R, o.token);
 }
@@ -1719,6 +2110,7 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
         d.slice_len = p.slice_len;
         d.row_begin = row_begin;
         d.recs = (char*)workspace + off;
+        d.paths = (uint32_t*)((char*)workspace + MIS_WS_PATH_OFFSET);
         off += (size_t)g.rows * p.S * kRecBytes;
         row_begin += g.rows;
         blocks += (int64_t)g.rows * p.S;
@@ -1727,7 +2119,6 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     if (blocks > 0 && (!workspace || off > workspace_bytes))
         return fail(MIS_E_WORKSPACE, "workspace too small: need %zu bytes, got %zu", off, workspace_bytes);
     if (blocks == 0) return 0;
-    a.status = (uint32_t*)workspace;
     a.arrive = (char*)workspace + kHeaderBytes;
     // whole rows to XCDs: contiguous in (group, row) order, balanced by slice count
     int64_t count[8] = {0, 0, 0, 0, 0, 0, 0, 0};

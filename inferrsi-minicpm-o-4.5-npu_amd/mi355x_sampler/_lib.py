@@ -21,6 +21,8 @@ MIS_RNG_COUNTER, MIS_RNG_PHILOX = 0, 1
 MIS_HISTORY_WINDOW, MIS_HISTORY_RING = 0, 1
 MIS_TOPK_ZERO_DISABLES, MIS_TOPP_ONE_DISABLES, MIS_UPDATE_STATE, MIS_FINALIZE_STREAMING = 1, 2, 4, 8
 MIS_E_ARG, MIS_E_WORKSPACE, MIS_E_UNSUPPORTED = 1, 2, 3
+MIS_WS_PATH_OFFSET = 64
+PATHS = ("greedy", "full", "candidates", "histogram", "stream", "forced")  # MIS_PATH_* order
 
 _vp = ctypes.c_void_p
 _i32, _i64, _f32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
@@ -103,17 +105,48 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
-# Workspace per (device, stream): launches sharing one must be stream-ordered.
+# Workspace per (device, stream): launches sharing one must be stream-ordered.  A buffer that is outgrown is kept
+# alive for the life of the process: a graph captured while it was current still writes to it on every replay.
 _ws: dict[tuple[int, int], torch.Tensor] = {}
+_retired: list[torch.Tensor] = []
+
+
+def _ws_key(device: torch.device) -> tuple[int, int]:
+    return (device.index if device.index is not None else torch.cuda.current_device(), stream_handle(device))
 
 
 def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream_handle(device))
+    key = _ws_key(device)
     buf = _ws.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _retired.append(buf)
         buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)  # counters start at zero
         _ws[key] = buf
     return buf
+
+
+def _path_words(device: torch.device) -> torch.Tensor | None:
+    buf = _ws.get(_ws_key(device))
+    if buf is None:
+        return None
+    return buf[MIS_WS_PATH_OFFSET:MIS_WS_PATH_OFFSET + 4 * len(PATHS)].view(torch.int32)
+
+
+def path_counters(device: torch.device) -> dict[str, int]:
+    """Rows finalised per path on the workspace of ``device``'s current stream since the last reset (diagnostics;
+    reads device memory, so it synchronises)."""
+    words = _path_words(device)
+    if words is None:
+        return dict.fromkeys(PATHS, 0)
+    v = words.cpu().tolist()
+    return {p: int(v[i]) for i, p in enumerate(PATHS)}
+
+
+def reset_path_counters(device: torch.device) -> None:
+    words = _path_words(device)
+    if words is not None:
+        words.zero_()
 
 
 def sample(groups: list[MisGroup], device: torch.device) -> None:

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from mi355x_sampler import _lib
 from mi355x_sampler import groups as G
 from mi355x_sampler import talker_sampler as hs
 from mi355x_sampler import workloads as W
@@ -56,13 +57,16 @@ WORKLOADS = [
 def test_workload_matches_oracle(name, make):
     wl = make()
     print(f"[gpu] workload {name}: rows={wl.rows} vocab={wl.vocab} dtype={wl.logits.dtype}", flush=True)
+    _lib.reset_path_counters(DEV)
     g = run(wl)
+    paths = _lib.path_counters(DEV)
     rows = oracle_rows(wl)
     ref = ext.sample_rows(rows)
     stats = compare_group(name, g.tokens, g.processed, g.probs, ref, rows,
                           prob_rtol=1e-5 if wl.logits.dtype == torch.float32 else 2e-3)
-    print(f"[gpu] {name}: {stats}", flush=True)
+    print(f"[gpu] {name}: {stats} paths {paths}", flush=True)
     assert stats["exact"] >= wl.rows - max(1, wl.rows // 16)
+    assert paths["stream"] == 0 and sum(paths.values()) == wl.rows
 
 
 STREAMING = [
@@ -123,10 +127,15 @@ def test_large_nucleus_second_pass(semantics):
     g = G.RowGroup(x.to(DEV), temperature=1.0, top_k=0, top_p=top_p.to(DEV), repetition=1.1, history=hist.to(DEV),
                    seeds=one(3, torch.int64).to(DEV), steps=one(1, torch.int64).to(DEV), eos=5, min_new_tokens=4,
                    semantics=semantics, min_keep=3 if semantics == "hf" else 1, processed=True, probs=True)
+    _lib.reset_path_counters(DEV)
     G.launch([g])
     torch.cuda.synchronize()
+    paths = _lib.path_counters(DEV)
+    print(f"[gpu] large nucleus {semantics} paths {paths}", flush=True)
     compare_group(f"large_nucleus_{semantics}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows,
                   prob_rtol=2e-3)
+    # the wide rows are settled from the slices' value histograms, none by streaming the row
+    assert paths["stream"] == 0 and paths["histogram"] >= 3 and sum(paths.values()) == rows
 
 
 def test_boundary_bin_and_candidate_rows_across_launches():
