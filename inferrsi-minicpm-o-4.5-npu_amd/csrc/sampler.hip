@@ -50,7 +50,9 @@ constexpr int kSpecCap = 2048;                   // specials of one slice
 constexpr int kCapWave = 512;                    // candidates one wave of a slice may publish
 constexpr int kCapSpecSeg = 512;                 // candidates among a slice's specials
 constexpr int kSegs = kWaves + 1;                // candidate segments of a slice: 16 waves + the specials
-constexpr int kCapRow = 12288;                   // candidates a finaliser gathers
+constexpr int kCapRow = 12288;                   // entries of the histogram path's weighted list
+constexpr int kCapCand = 6144;                   // candidates a finaliser gathers (with their masses)
+constexpr int kCapSmall = 1024;                  // a narrowed candidate set
 constexpr int kBins = 2048;                      // radix digit: 11 bits
 constexpr int kMaxSB = kWaves * kRounds;         // (wave, round) sub-blocks of a slice
 constexpr double kFx = 4398046511104.0;          // 2^42 fixed-point units of exp(q - max): V * 2^42 < 2^64
@@ -162,23 +164,38 @@ struct Hist {
     unsigned long long before;
 };
 
+struct SmallSet {
+    float q[kCapSmall];
+    uint32_t id[kCapSmall];
+    unsigned long long mass[kCapSmall];
+};
+
 // LDS of one workgroup.  The slice phase and the finaliser overlay the big arrays.
 struct Lds {
     union {
         uint32_t cnt[kCntWords];  // slice phase / streaming: history counts by position (u16 pairs)
         struct {
             float q[kCapRow];
-            uint32_t id[kCapRow];
-        } c;                      // finaliser: gathered candidates
+            uint32_t id[kCapRow];  // multiplicity (weighted lists)
+        } c;                       // finaliser: histogram path, streaming
+        struct {
+            float q[kCapCand];
+            uint32_t id[kCapCand];
+            unsigned long long mass[kCapCand];  // efx(q, row max)
+        } w;                       // finaliser: gathered candidates
     } a;
     Hist h;
     uint32_t keep[kKeepWords];
-    Special spec[kSpecCap];
+    union {
+        Special spec[kSpecCap];  // slice phase
+        SmallSet sm[2];          // finaliser: narrowed candidate sets (compaction alternates between the two)
+    };
     double sb[kMaxSB];
     unsigned long long sbfx[kMaxSB];
     int32_t segoff[kMaxSlices * kSegs + 1];
     Red red;
     int32_t nspec;
+    int32_t scnt;
     int32_t flags;
     int32_t is_last;
     int32_t foreign;
@@ -598,6 +615,17 @@ __device__ __forceinline__ void append_cand(bool pred, QF&& qf, uint32_t j, unsi
     cnt += n;
 }
 
+// Room in an LDS list for the lanes where pred holds (wave-aggregated); -1 where it does not.
+__device__ __forceinline__ int lds_reserve(bool pred, int* counter) {
+    const uint64_t b = ballot(pred);
+    if (b == 0ull) return -1;
+    const int leader = __ffsll((long long)b) - 1;
+    int base = 0;
+    if (lane_id() == leader) base = atomicAdd(counter, __popcll(b));
+    base = __builtin_amdgcn_readlane(base, leader);
+    return pred ? base + (int)rank_below(b) : -1;
+}
+
 // bf16 pairs with the halves whose keep bit is clear set to -inf (0xFF80).
 __device__ __forceinline__ uint32_t mask_pair(uint32_t v, uint32_t kb, int d) {
     const uint32_t lo = (kb >> (2 * d)) & 1u, hi = (kb >> (2 * d + 1)) & 1u;
@@ -613,6 +641,18 @@ template <int ES>
 __device__ __forceinline__ float tile_val(const uint4& v, int e) {
     if (ES == 2) {
         const uint32_t w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+        return (e & 1) ? bf_hi(w) : bf_lo(w);
+    }
+    const uint32_t w = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+    return __uint_as_float(w);
+}
+
+// tile_val for an element index known only at run time.
+template <int ES>
+__device__ __forceinline__ float tile_val_dyn(const uint4& v, int e) {
+    if (ES == 2) {
+        const int k = e >> 1;
+        const uint32_t w = k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w;
         return (e & 1) ? bf_hi(w) : bf_lo(w);
     }
     const uint32_t w = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
@@ -720,6 +760,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     if (tid == 0) {
         L.flags = 0;
         L.nspec = 0;
+        L.scnt = 0;
     }
     if (tid < kMaxSB) L.sbfx[tid] = 0ull;
     __syncthreads();
@@ -842,7 +883,12 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         return arrive(A, R, L) ? kActFinalize : kActNone;
     }
 
-    const float4 mx = block_max4(make_float4(lmax, smax, sdmax, -INFINITY), L.red);
+    // top-k and top-p rows: each wave's gate (c lane maxima at or above it); the slice publishes every element at or
+    // above the highest of them (the finaliser needs its cut at or above the highest gate of the row anyway, so
+    // elements below it are never used), folded into the maxima's reduction
+    const bool gated = R.mode == kTopK || R.mode == kNucleus;
+    const float wgate = gated ? wave_gate(lmax, R.c_gate) : -INFINITY;
+    const float4 mx = block_max4(make_float4(lmax, smax, sdmax, wgate), L.red);
     const float tmq = is_finite_f(mx.x) ? to_q<ES>(R, mx.x) : mx.x;  // tile max, processed domain
     const float mq = fmaxf(tmq, mx.y);
     const float mqd = fmaxf(tmq, mx.z);
@@ -892,7 +938,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     }
 
     // top-k and top-p rows: per-wave gates; every element of the wave at or above its gate is published
-    const float gate = wave_gate(lmax, R.c_gate);
+    const float gate = mx.w;  // the slice's gate, in the tile's domain
     const float gate_q = (gate > -INFINITY) ? to_q<ES>(R, gate) : -INFINITY;
     unsigned long long* segs = (unsigned long long*)((char*)rec + kRecCandOff);
     unsigned long long* myseg = segs + (int64_t)w * kCapWave;
@@ -911,25 +957,60 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     for (int r = 0; r < RMAX; ++r) {
         if (r >= RR) continue;
         const int c = (w * RR + r) * 64 + l;
+        // the chunk's elements at or above the gate as a mask; one wave scan places every lane's candidates (in
+        // token order) after the wave's previous ones
+        uint32_t bits = 0u;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             const float x = tile_val<ES>(t[r], e);
-            const bool pred = x >= gate && x > -INFINITY;
-            const uint32_t j = (uint32_t)(geo.first + c * E + e);
+            bits |= (x >= gate && x > -INFINITY) ? (1u << e) : 0u;
             if (R.needz) {
                 const float q = to_q<ES>(R, x);
                 if (q > -INFINITY) zacc += (double)exp_acc(q - mref);
-                append_cand(pred, [&] { return q; }, j, myseg, kCapWave, cnt, flags);
+            }
+        }
+        const int nb = __popc(bits);
+        const int incl = wave_incl_scan(nb);
+        const int tot = __builtin_amdgcn_readlane(incl, 63);
+        if (tot) {
+            if (cnt + tot > kCapWave) {
+                flags |= kRecOverflow;
+                cnt = kCapWave;
             } else {
-                append_cand(pred, [&] { return to_q<ES>(R, x); }, j, myseg, kCapWave, cnt, flags);
+                int pos = cnt + incl - nb;
+                const uint32_t j0 = (uint32_t)(geo.first + c * E);
+                while (bits) {
+                    const int e = __ffs(bits) - 1;
+                    bits &= bits - 1u;
+                    const float q = to_q<ES>(R, tile_val_dyn<ES>(t[r], e));
+                    myseg[pos++] = ((unsigned long long)(j0 + (uint32_t)e) << 32) | __float_as_uint(q);
+                }
+                cnt += tot;
             }
         }
     }
+    // specials at or above the gate (every wave; slots of segment kWaves reserved in LDS)
+    unsigned long long* sseg = segs + (int64_t)kWaves * kCapWave;
+    for (int i0 = 0; i0 < ns; i0 += kThreads) {
+        const int i = i0 + tid;
+        const bool in = i < ns;
+        const float q = in ? L.spec[i].q : -INFINITY;
+        const uint32_t id = in ? ((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) : 0u;
+        if (R.needz && q > -INFINITY) zacc += (double)exp_acc(q - mref);
+        const bool pred = q >= gate_q && q > -INFINITY;
+        const int slot = lds_reserve(pred, &L.scnt);
+        if (pred) {
+            if (slot < kCapSpecSeg)
+                sseg[slot] = ((unsigned long long)id << 32) | __float_as_uint(q);
+            else
+                flags |= kRecOverflow;
+        }
+    }
     if (R.needz) zacc = wave_reduce(zacc, [](double a, double b) { return a + b; });
+    flags = wave_reduce(flags, [](int a, int b) { return a | b; });
     __syncthreads();
     if (l == 0) {
         L.segoff[w] = cnt;
-        L.red.f[w] = gate_q;
         L.red.d[w] = zacc;
         if (flags) atomicOr(&L.flags, flags);
     }
@@ -967,42 +1048,20 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             sg[i] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
                     __float_as_uint(L.spec[i].q);
     }
-    float gs = -INFINITY;
-    double z = 0.0;
+    if (tid == 0) {
+        double z = 0.0;
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
-        gs = fmaxf(gs, L.red.f[i]);
-        z += L.red.d[i];
-    }
-    // specials at or above their wave's gate: segment kWaves, written by wave 0
-    if (w == 0) {
-        int scnt = 0, sflags = 0;
-        unsigned long long* sseg = segs + (int64_t)kWaves * kCapWave;
-        double sz = 0.0;
-        for (int b = 0; b < ns; b += 64) {
-            const int i = b + l;
-            const bool in = i < ns;
-            const float q = in ? L.spec[i].q : -INFINITY;
-            const int j = in ? L.spec[i].j : 0;
-            const int sw = in ? ((j - geo.first) / (E * RR * 64)) : 0;
-            const bool pred = in && q >= L.red.f[sw] && q > -INFINITY;
-            if (R.needz && in && q > -INFINITY) sz += (double)exp_acc(q - mref);
-            const uint32_t id = (uint32_t)j | ((in && L.spec[i].sel) ? kSelOnlyBit : 0u);
-            append_cand(pred, [&] { return q; }, id, sseg, kCapSpecSeg, scnt, sflags);
-        }
-        sz = wave_reduce(sz, [](double a, double b) { return a + b; });
-        if (l == 0) {
-            rec->ncand[kWaves] = scnt;
-            rec->mq = mq;
-            rec->mqd = mqd;
-            rec->gate = gs;
-            rec->mref = mref;
-            rec->z = z + sz;
-            rec->flags = L.flags | sflags | (gs > -INFINITY ? 0 : kRecGateInf);
-            rec->hist = hist ? 1 : 0;
-            rec->nspec = ns;
-            rec->tinyfx = L.tinyfx;
-        }
+        for (int i = 0; i < kWaves; ++i) z += L.red.d[i];
+        rec->ncand[kWaves] = min(L.scnt, kCapSpecSeg);
+        rec->mq = mq;
+        rec->mqd = mqd;
+        rec->gate = gate_q;
+        rec->mref = mref;
+        rec->z = z;
+        rec->flags = L.flags | (gate_q > -INFINITY ? 0 : kRecGateInf);
+        rec->hist = hist ? 1 : 0;
+        rec->nspec = ns;
+        rec->tinyfx = L.tinyfx;
     }
     if (tid < kWaves) rec->ncand[tid] = L.segoff[tid];
     return arrive(A, R, L) ? kActFinalize : kActNone;
@@ -1191,7 +1250,7 @@ __device__ __forceinline__ bool range_find(Visit& V, int sel, bool desc, unsigne
     for (;;) {
         const uint64_t span = (uint64_t)khi - klo + 1;
         int sh = 0;
-        while ((span >> sh) > (uint64_t)kBins) ++sh;
+        while (((span - 1) >> sh) >= (uint64_t)kBins) ++sh;  // every key's bin (key - klo) >> sh < kBins
         const int nb = (int)((span + ((1ull << sh) - 1)) >> sh);
         for (int b = threadIdx.x; b < nb; b += kThreads) h.w[b] = 0ull;
         __syncthreads();
@@ -1383,44 +1442,448 @@ __device__ __forceinline__ double block_incl_scan_d(double x, Red& r) {
     return off + incl;
 }
 
-// Candidate rows: gather every slice's candidates into LDS, select, draw.  False: stream instead.
-__device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
-    const int S = R.S;
-    const int nseg = S * kSegs;
-    // the records: thread s reads slice s; thread t reads segment counts 2t and 2t + 1
-    float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
-    double zz = 0.0;
-    int over = 0, notinf = 0;
-    if ((int)threadIdx.x < S) {
-        const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, threadIdx.x);
-        mq = pub_ld(&rec->mq);
-        gt = pub_ld(&rec->gate);
-        mr = pub_ld(&rec->mref);
-        zz = pub_ld(&rec->z);
-        const int fl = pub_ld(&rec->flags);
-        over = (fl & kRecOverflow) ? 1 : 0;
-        notinf = (fl & kRecGateInf) ? 0 : 1;
-    }
-    int c0 = 0, c1 = 0;
-    const int i0 = 2 * (int)threadIdx.x, i1 = i0 + 1;
-    if (i0 < nseg) c0 = pub_ld(&((const SliceRec*)rec_base(G, R.row, i0 / kSegs))->ncand[i0 % kSegs]);
-    if (i1 < nseg) c1 = pub_ld(&((const SliceRec*)rec_base(G, R.row, i1 / kSegs))->ncand[i1 % kSegs]);
-    const float4 m4 = block_max4(make_float4(mq, gt, over ? 1.f : 0.f, notinf ? 1.f : 0.f), L.red);
-    const float m_sel = m4.x, gate = m4.y;
-    if (m4.z > 0.f) return false;
-    const bool all_inf = !(m4.w > 0.f);
-    double zs = 0.0;
-    if (R.needz)
-        zs = block_sum_d((mr > -INFINITY && m_sel > -INFINITY) ? zz * exp((double)mr - (double)m_sel) : 0.0, L.red);
+// ------------------------------------------------------------------ the candidate finaliser (one wave)
+//
+// Once the candidates are in LDS (gathered by the whole workgroup, each with its mass relative to the row max), the
+// selections run on wave 0 alone: no workgroup barriers, and each instruction costs one issue slot instead of
+// sixteen.  The other waves wait at the barrier that follows.
+
+// LDS written by this wave is visible to its other lanes (wave-level ordering only: no s_barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long x, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+#define MIS_LDS __attribute__((address_space(3)))
+
+// A candidate set in LDS: value, id (with kSelOnlyBit), mass efx(q, row max).  The pointers carry the LDS address
+// space so that every access is a DS instruction, not a flat one.
+struct WSet {
+    const MIS_LDS float* q;
+    const MIS_LDS uint32_t* id;
+    const MIS_LDS unsigned long long* mass;
     int n;
-    const int ex = block_excl_scan(c0 + c1, n, L.red.i);
-    if (i0 < nseg) L.segoff[i0] = ex;
-    if (i1 < nseg) L.segoff[i1] = ex + c0;
-    if (threadIdx.x == 0) L.segoff[nseg] = n;
+};
+
+__device__ __forceinline__ WSet wset_of(float* q, uint32_t* id, unsigned long long* mass, int n) {
+    WSet s;
+    s.q = (const MIS_LDS float*)q;
+    s.id = (const MIS_LDS uint32_t*)id;
+    s.mass = (const MIS_LDS unsigned long long*)mass;
+    s.n = n;
+    return s;
+}
+
+// What a selection counts: kSelCount (finite values), kSelCut (mass above kth), kSelDraw (keys are ids; survivors'
+// mass relative to md).
+struct WSel {
+    int sel;
+    float kth, thr, md;
+    bool md_is_m;  // md is the row max: the stored masses serve the draw
+};
+
+// Every field is loaded unconditionally and combined with selects: a load under a divergent condition is followed
+// by its own wait, and one wave has nothing else to run meanwhile.
+__device__ __forceinline__ void wentry(const WSet& s, int i, const WSel& P, uint32_t& key, unsigned long long& w) {
+    const float q = s.q[i];
+    const uint32_t id = s.id[i];
+    const unsigned long long m = s.mass[i];
+    if (P.sel == kSelDraw) {
+        key = id & ~kSelOnlyBit;
+        const unsigned long long wm = P.md_is_m ? m : efx(q, P.md);
+        w = (!(id & kSelOnlyBit) && q >= P.thr) ? wm : 0ull;
+    } else {
+        key = ord_key(q);
+        w = P.sel == kSelCount ? (q > -INFINITY ? 1ull : 0ull) : (q > P.kth ? m : 0ull);
+    }
+}
+
+// The entries of s where pred(i) holds, copied into whichever of L.sm[0], L.sm[1] s is not (so never in place),
+// or s itself when they do not fit.  Four entries per lane per step, so that their LDS reads overlap.
+template <class Pred>
+__device__ __forceinline__ WSet wcompact(const WSet& s, Pred pred, Lds& L) {
+    const int l = lane_id();
+    const bool in0 = s.q == (const MIS_LDS float*)L.sm[0].q;
+    MIS_LDS float* dq = (MIS_LDS float*)(in0 ? L.sm[1].q : L.sm[0].q);
+    MIS_LDS uint32_t* did = (MIS_LDS uint32_t*)(in0 ? L.sm[1].id : L.sm[0].id);
+    MIS_LDS unsigned long long* dm = (MIS_LDS unsigned long long*)(in0 ? L.sm[1].mass : L.sm[0].mass);
+    int cnt = 0;
+    for (int i0 = 0; i0 < s.n; i0 += 256) {
+        bool p[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + 64 * u + l;
+            p[u] = pred(min(i, s.n - 1)) && i < s.n;  // clamped: the reads are unconditional and overlap
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) cnt += __popcll(ballot(p[u]));
+    }
+    if (cnt > kCapSmall) return s;
+    int base = 0;
+    for (int i0 = 0; i0 < s.n; i0 += 256) {
+        bool p[4];
+        float q[4];
+        uint32_t id[4];
+        unsigned long long m[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + 64 * u + l, ic = min(i, s.n - 1);
+            p[u] = pred(ic) && i < s.n;
+            q[u] = s.q[ic];
+            id[u] = s.id[ic];
+            m[u] = s.mass[ic];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const uint64_t b = ballot(p[u]);
+            if (p[u]) {
+                const int slot = base + (int)rank_below(b);
+                dq[slot] = q[u];
+                did[slot] = id[u];
+                dm[slot] = m[u];
+            }
+            base += __popcll(b);
+        }
+    }
+    wave_lds_sync();
+    WSet r;
+    r.q = dq;
+    r.id = did;
+    r.mass = dm;
+    r.n = cnt;
+    return r;
+}
+
+// f(i, valid) for i = lane, lane + 64, ... < n, four per lane per step with clamped (always valid) indices.
+template <class F>
+__device__ __forceinline__ void wave_for(int n, F f) {
+    const int l = lane_id();
+    for (int i0 = 0; i0 < n; i0 += 256) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + 64 * u + l;
+            f(min(i, n - 1), i < n);
+        }
+    }
+}
+
+template <class T>
+__device__ __forceinline__ T wave_sum(T x) {
+    return wave_reduce(x, [](T a, T b) { return a + b; });
+}
+
+// One round of a wave selection: 256 bins, lane l holding bins 4l .. 4l + 3 (scan order: descending visits bins
+// 255 .. 0, ascending 0 .. 255; bins past the range are empty).  Returns the bin where the cumulative weight
+// reaches T and the weight before it, or -1 when the total is below T.
+template <class BinOf>
+__device__ __forceinline__ int wround(const WSet& s, const WSel& P, bool desc, unsigned long long T, uint32_t klo,
+                                      uint32_t khi, uint32_t vkey, unsigned long long vw, BinOf bin_of, Lds& L,
+                                      unsigned long long& before) {
+    const int l = lane_id();
+    unsigned long long* bins = L.h.w;
+    ulonglong2* bins2 = (ulonglong2*)L.h.w;
+    bins2[2 * l] = make_ulonglong2(0ull, 0ull);
+    bins2[2 * l + 1] = make_ulonglong2(0ull, 0ull);
+    wave_lds_sync();
+    for (int i0 = 0; i0 < s.n; i0 += 256) {
+        uint32_t key[4];
+        unsigned long long w[4];
+        float q[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + 64 * u + l, ic = min(i, s.n - 1);
+            wentry(s, ic, P, key[u], w[u]);
+            q[u] = s.q[ic];
+            if (i >= s.n) w[u] = 0ull;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (w[u] && key[u] >= klo && key[u] <= khi) atomicAdd(&bins[bin_of(key[u], q[u])], w[u]);
+    }
+    if (l == 0 && vw && vkey >= klo && vkey <= khi) atomicAdd(&bins[bin_of(vkey, key_float(vkey))], vw);
+    wave_lds_sync();
+    unsigned long long v[4];
+    if (desc) {
+        const ulonglong2 hi = bins2[127 - 2 * l], lo = bins2[126 - 2 * l];
+        v[0] = hi.y;
+        v[1] = hi.x;
+        v[2] = lo.y;
+        v[3] = lo.x;
+    } else {
+        const ulonglong2 a = bins2[2 * l], b = bins2[2 * l + 1];
+        v[0] = a.x;
+        v[1] = a.y;
+        v[2] = b.x;
+        v[3] = b.y;
+    }
+    wave_lds_sync();  // read before the next round clears them
+    const unsigned long long sum = v[0] + v[1] + v[2] + v[3];
+    const unsigned long long incl = wave_incl_scan(sum);
+    if (readlane_u64(incl, 63) < T) return -1;
+    const unsigned long long ex = incl - sum;
+    const int ls = __ffsll((long long)ballot(ex < T && T <= incl)) - 1;
+    int t = 3;
+    unsigned long long bef = ex + v[0] + v[1] + v[2];
+    if (ex + v[0] >= T) {
+        t = 0;
+        bef = ex;
+    } else if (ex + v[0] + v[1] >= T) {
+        t = 1;
+        bef = ex + v[0];
+    } else if (ex + v[0] + v[1] + v[2] >= T) {
+        t = 2;
+        bef = ex + v[0] + v[1];
+    }
+    const int pos = 4 * ls + __builtin_amdgcn_readlane(t, ls);
+    before = readlane_u64(bef, ls);
+    return desc ? 255 - pos : pos;
+}
+
+// range_find on one wave over a candidate set: the first key (descending or ascending within [klo, khi]) at which
+// the cumulative weight, with the virtual element (vkey, vw), reaches T (T >= 1); false when the total is below T.
+// A large set of values is first binned linearly by value (monotone, so the chosen bin is a value interval; keys
+// of clustered values would pile onto a few bins and serialise the LDS atomics), narrowed to that bin's entries,
+// and then binned by key, 256 bins a round.
+__device__ __forceinline__ bool wsel(WSet s, const WSel& P, bool desc, unsigned long long T, uint32_t klo,
+                                     uint32_t khi, uint32_t vkey, unsigned long long vw, Lds& L, uint32_t& key_out,
+                                     unsigned long long& before_out) {
+    const int l = lane_id();
+    unsigned long long acc = 0ull, bef = 0ull;
+    if (P.sel != kSelDraw && s.n > 64 && khi > klo) {
+        const float qlo = key_float(klo), qhi = key_float(khi);
+        const float scale = 256.0f / (qhi - qlo);
+        if (scale > 0.0f && scale < INFINITY) {
+            auto vbin = [=](uint32_t, float q) { return min(255, (int)((q - qlo) * scale)); };
+            const int b = wround(s, P, desc, T, klo, khi, vkey, vw, vbin, L, bef);
+            if (b < 0) return false;
+            T -= bef;
+            acc += bef;
+            // the entries (and the virtual element) in bin b: their keys bound the next rounds
+            uint32_t kmin = 0xffffffffu, kmax = 0u;
+            auto in_b = [&](int i) {
+                uint32_t key;
+                unsigned long long w;
+                wentry(s, i, P, key, w);
+                return key >= klo && key <= khi && vbin(key, s.q[i]) == b;
+            };
+            wave_for(s.n, [&](int i, bool ok) {
+                const bool c = in_b(i) && ok;
+                const uint32_t k = ord_key(s.q[i]);
+                kmin = min(kmin, c ? k : 0xffffffffu);
+                kmax = max(kmax, c ? k : 0u);
+            });
+            if (l == 0 && vw && vkey >= klo && vkey <= khi && vbin(vkey, key_float(vkey)) == b) {
+                kmin = min(kmin, vkey);
+                kmax = max(kmax, vkey);
+            }
+            kmin = wave_reduce(kmin, [](uint32_t a, uint32_t c) { return min(a, c); });
+            kmax = wave_reduce(kmax, [](uint32_t a, uint32_t c) { return max(a, c); });
+            klo = kmin;
+            khi = kmax;
+            s = wcompact(s, in_b, L);
+        }
+    }
+    for (;;) {
+        const uint64_t span = (uint64_t)khi - klo + 1;
+        int sh = 0;
+        while (((span - 1) >> sh) >= 256ull) ++sh;  // every key's bin (key - klo) >> sh < 256
+        const uint32_t base = klo;
+        const int b = wround(s, P, desc, T, klo, khi, vkey, vw, [=](uint32_t k, float) { return (int)((k - base) >> sh); },
+                             L, bef);
+        if (b < 0) return false;
+        T -= bef;
+        acc += bef;
+        const uint64_t a = (uint64_t)klo + ((uint64_t)b << sh);
+        klo = (uint32_t)a;
+        khi = (uint32_t)std::min<uint64_t>((uint64_t)khi, a + (1ull << sh) - 1);
+        if (sh == 0) break;
+        if (s.n > 64 && s.q == (const MIS_LDS float*)L.a.w.q) {  // narrow the gathered set once
+            const uint32_t lo_k = klo, hi_k = khi;
+            s = wcompact(s, [&](int i) {
+                uint32_t key;
+                unsigned long long w;
+                wentry(s, i, P, key, w);
+                return key >= lo_k && key <= hi_k;
+            }, L);
+        }
+    }
+    key_out = klo;
+    before_out = acc;
+    return true;
+}
+
+// select_draw for the candidate set s on wave 0 (same selections, same checks against the gate).
+__device__ __forceinline__ bool wselect_draw(const Row& R, Lds& L, WSet s, float m_sel, double zfull_fx, float gate,
+                                             bool all_gate_inf, uint32_t klo, uint32_t khi, float u, Outcome& out) {
+    const int l = lane_id();
+    const int n_fin = s.n;
+    const bool topk = R.kk < R.V;
+    WSel P;
+    P.kth = P.thr = P.md = -INFINITY;
+    P.md_is_m = true;
+    float kth = -INFINITY;
+    unsigned long long cnt_gt = (unsigned long long)n_fin;
+    uint32_t key = 0u;
+    unsigned long long bf = 0ull;
+    if (topk) {
+        if ((unsigned long long)R.kk <= (unsigned long long)n_fin) {
+            P.sel = kSelCount;
+            wsel(s, P, true, (unsigned long long)R.kk, klo, khi, 0u, 0ull, L, key, bf);
+            kth = key_float(key);
+            cnt_gt = bf;
+            if (!(kth >= gate)) return false;
+            s = wcompact(s, [&](int i) { return s.q[i] >= kth; }, L);  // the top-k set (ties included)
+            klo = key;
+        } else if (!all_gate_inf) {
+            return false;
+        }
+    }
+    float thr = kth;
+    if (R.p_active) {
+        P.kth = kth;
+        const unsigned long long ekth = efx(kth, m_sel);
+        const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
+        double zn;
+        if (topk && !R.hf) {
+            unsigned long long a = 0ull;
+            wave_for(s.n, [&](int i, bool ok) {
+                const float q = s.q[i];
+                const unsigned long long m = s.mass[i];
+                a += (ok && q > kth) ? m : 0ull;
+            });
+            zn = (double)(wave_sum(a) + vw);
+        } else {
+            zn = zfull_fx;
+        }
+        const double pt = ceil((double)R.top_p * zn);
+        const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+        const uint32_t kthkey = ord_key(kth);
+        P.sel = kSelCut;
+        const bool found = wsel(s, P, true, T, (kth > -INFINITY) ? max(klo, kthkey) : klo, khi, kthkey, vw, L, key, bf);
+        float thr_p;
+        if (found) {
+            thr_p = key_float(key);
+        } else {
+            if (!topk) return false;  // the nucleus reaches below the candidates
+            thr_p = kth;
+        }
+        if (!topk && !(thr_p >= gate)) return false;
+        float vmk = m_sel;
+        if (R.min_keep_eff >= 2) {
+            if ((unsigned long long)R.min_keep_eff > (unsigned long long)n_fin) {
+                vmk = -INFINITY;
+            } else {
+                P.sel = kSelCount;
+                wsel(s, P, true, (unsigned long long)R.min_keep_eff, klo, khi, 0u, 0ull, L, key, bf);
+                vmk = key_float(key);
+                if (!(vmk >= gate)) return false;
+            }
+        }
+        thr = fminf(thr_p, vmk);
+        if (topk) thr = fmaxf(thr, kth);
+    }
+    // survivors: drawable, finite, q >= thr
+    s = wcompact(s, [&](int i) { return !(s.id[i] & kSelOnlyBit) && s.q[i] >= thr && s.q[i] > -INFINITY; }, L);
+    float md = -INFINITY;
+    wave_for(s.n, [&](int i, bool ok) {
+        const float q = s.q[i];
+        const uint32_t id = s.id[i];
+        md = fmaxf(md, (ok && !(id & kSelOnlyBit) && q >= thr) ? q : -INFINITY);
+    });
+    md = wave_reduce(md, [](float a, float b) { return fmaxf(a, b); });
+    out.thr = thr;
+    out.mdraw = md;
+    out.token = R.V - 1;
+    if (!(md > -INFINITY)) return true;
+    P.sel = kSelDraw;
+    P.thr = thr;
+    P.md = md;
+    P.md_is_m = md == m_sel;
+    unsigned long long zs = 0ull;
+    wave_for(s.n, [&](int i, bool ok) {
+        uint32_t k;
+        unsigned long long w;
+        wentry(s, i, P, k, w);
+        zs += ok ? w : 0ull;
+    });
+    zs = wave_sum(zs);
+    const unsigned long long T = (unsigned long long)floor((double)u * (double)zs) + 1ull;
+    if (zs > 0ull && wsel(s, P, false, T, 0u, (uint32_t)(R.V - 1), 0u, 0ull, L, key, bf)) out.token = (int64_t)key;
+    return true;
+}
+
+// Candidate rows: every slice's candidates gathered into LDS (the whole workgroup), then selected and drawn on
+// wave 0.  False: the histogram path or streaming instead.
+__device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
+    const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
+    const int nseg = S * kSegs;
+    if (w == 0) {
+        // records (lane s: slice s) and segment counts (lane l: segments [l * per, (l + 1) * per))
+        const float u = row_uniform(G, R);
+        float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
+        double zz = 0.0;
+        int over = 0, notinf = 0;
+        if (l < S) {
+            const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
+            mq = pub_ld(&rec->mq);
+            gt = pub_ld(&rec->gate);
+            mr = pub_ld(&rec->mref);
+            zz = pub_ld(&rec->z);
+            const int fl = pub_ld(&rec->flags);
+            over = (fl & kRecOverflow) ? 1 : 0;
+            notinf = (fl & kRecGateInf) ? 0 : 1;
+        }
+        const int per = (nseg + 63) >> 6;
+        int c[kSegs];
+        int mine = 0;
+#pragma unroll
+        for (int t = 0; t < kSegs; ++t) {
+            const int i = l * per + t;
+            c[t] = (t < per && i < nseg) ? pub_ld(&((const SliceRec*)rec_base(G, R.row, i / kSegs))->ncand[i % kSegs]) : 0;
+            mine += c[t];
+        }
+        const float m_sel = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
+        const float gate = wave_reduce(gt, [](float a, float b) { return fmaxf(a, b); });
+        const int anyover = wave_reduce(over, [](int a, int b) { return max(a, b); });
+        const int anyfin = wave_reduce(notinf, [](int a, int b) { return max(a, b); });
+        double zs = 0.0;
+        if (R.needz)
+            zs = wave_sum((mr > -INFINITY && m_sel > -INFINITY) ? zz * exp((double)mr - (double)m_sel) : 0.0);
+        const int incl = wave_incl_scan(mine);
+        int o = incl - mine;
+#pragma unroll
+        for (int t = 0; t < kSegs; ++t) {
+            const int i = l * per + t;
+            if (t < per && i < nseg) L.segoff[i] = o;
+            o += c[t];
+        }
+        if (l == 0) {
+            const int n = __builtin_amdgcn_readlane(incl, 63);
+            L.segoff[nseg] = n;
+            L.fscratch[0] = m_sel;
+            L.fscratch[1] = gate;
+            L.fscratch[2] = u;
+            L.dscratch[0] = zs;
+            L.token = anyover;
+            L.is_last = anyfin;
+            L.uscratch[0] = 0xffffffffull;  // min key, max key of the candidates (below)
+            L.uscratch[1] = 0ull;
+        }
+    }
     __syncthreads();
-    if (n > kCapRow) return false;
-    float qmax = -INFINITY, nqmin = -INFINITY;
-    for (int i = threadIdx.x; i < n; i += kThreads) {
+    const int n = L.segoff[nseg];
+    if (L.token || n > kCapCand) return false;
+    const float m_sel = L.fscratch[0];
+    // gather, with each candidate's mass relative to the row max
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    for (int i = tid; i < n; i += kThreads) {
         int lo = 0, hi = nseg;  // segment: segoff[lo] <= i < segoff[lo + 1]
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
@@ -1434,31 +1897,39 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
             (const unsigned long long*)(rec_base(G, R.row, s) + kRecCandOff) + (int64_t)sg * kCapWave;
         const unsigned long long v = pub_ld(seg + (i - L.segoff[lo]));
         const float q = __uint_as_float((uint32_t)v);
-        L.a.c.q[i] = q;
-        L.a.c.id[i] = (uint32_t)(v >> 32);
-        qmax = fmaxf(qmax, q);
-        nqmin = fmaxf(nqmin, -q);
+        L.a.w.q[i] = q;
+        L.a.w.id[i] = (uint32_t)(v >> 32);
+        L.a.w.mass[i] = efx(q, m_sel);
+        const uint32_t k = ord_key(q);
+        kmin = min(kmin, k);
+        kmax = max(kmax, k);
     }
-    const float4 ext = block_max4(make_float4(qmax, nqmin, -INFINITY, -INFINITY), L.red);
-    const uint32_t klo = n ? ord_key(-ext.y) : 0u, khi = n ? ord_key(ext.x) : 0u;
-    Visit V;
-    V.weighted = false;
-    V.src = kSrcCands;
-    V.n = n;
-    V.lo = V.hi = 0;
-    V.kth = V.thr = V.m = V.md = -INFINITY;
-    return select_draw(G, R, L, V, m_sel, zs * kFx, n, gate, all_inf, true, klo, khi, out);
-}
-
-// Room in the finaliser's LDS list for the lanes where pred holds (wave-aggregated); -1 where it does not.
-__device__ __forceinline__ int lds_reserve(bool pred, int* counter) {
-    const uint64_t b = ballot(pred);
-    if (b == 0ull) return -1;
-    const int leader = __ffsll((long long)b) - 1;
-    int base = 0;
-    if (lane_id() == leader) base = atomicAdd(counter, __popcll(b));
-    base = __builtin_amdgcn_readlane(base, leader);
-    return pred ? base + (int)rank_below(b) : -1;
+    kmin = wave_reduce(kmin, [](uint32_t a, uint32_t b) { return min(a, b); });
+    kmax = wave_reduce(kmax, [](uint32_t a, uint32_t b) { return max(a, b); });
+    if (l == 0 && n) {
+        atomicMin((unsigned long long*)&L.uscratch[0], (unsigned long long)kmin);
+        atomicMax((unsigned long long*)&L.uscratch[1], (unsigned long long)kmax);
+    }
+    __syncthreads();
+    if (w == 0) {
+        const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
+        const uint32_t klo = n ? (uint32_t)L.uscratch[0] : 0u, khi = n ? (uint32_t)L.uscratch[1] : 0u;
+        Outcome o;
+        const bool ok = wselect_draw(R, L, s, m_sel, L.dscratch[0] * kFx, L.fscratch[1], L.is_last == 0, klo, khi,
+                                     L.fscratch[2], o);
+        if (l == 0) {
+            L.token = ok ? 1 : 0;
+            L.fscratch[3] = o.thr;
+            L.dscratch[1] = o.mdraw;
+            L.uscratch[0] = (unsigned long long)o.token;
+        }
+    }
+    __syncthreads();
+    if (!L.token) return false;
+    out.thr = L.fscratch[3];
+    out.mdraw = (float)L.dscratch[1];
+    out.token = (int64_t)L.uscratch[0];
+    return true;
 }
 
 // Top-p rows without top-k on bf16 logits whose nucleus the candidates do not hold.  The cut comes from every
