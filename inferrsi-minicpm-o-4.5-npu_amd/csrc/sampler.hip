@@ -193,6 +193,7 @@ struct Lds {
     double sb[kMaxSB];
     unsigned long long sbfx[kMaxSB];
     int32_t segoff[kMaxSlices * kSegs + 1];
+    alignas(16) uint32_t gh[256];  // slice phase: histogram of the lane maxima (the gate)
     Red red;
     int32_t nspec;
     int32_t scnt;
@@ -279,13 +280,12 @@ __device__ __forceinline__ Row make_row(const DevGroup& G, int gi, int row, int 
     R.eos_rule = !censor ? kEosNormal
                          : (!R.hf ? kEosExcluded : ((R.filters && (topk || R.p_active)) ? kEosSelOnly : kEosExcluded));
     R.needz = R.mode == kNucleus || (R.mode == kTopK && R.hf && R.p_active);
-    // lane maxima per wave the gate keeps: the row's k, up to 64 (then the wave's own top k are all published), else
-    // twice the wave's expected share of the top k plus 8; 16 for top-p rows without top-k
-    const int span_w = 64 * (16 / G.es) * G.R;
+    // lane maxima of the slice its gate keeps: the row's k up to 64 (then the slice's own top k are all published),
+    // else twice the slice's expected share of the top k plus 12; 64 for top-p rows without top-k
     if (R.mode == kTopK)
-        R.c_gate = R.kk <= 64 ? R.kk : min(48, (int)((2ll * R.kk * span_w + R.V - 1) / R.V) + 8);
+        R.c_gate = R.kk <= 64 ? R.kk : min(kThreads, (int)((2ll * R.kk * G.slice_len + R.V - 1) / R.V) + 12);
     else
-        R.c_gate = 16;
+        R.c_gate = 64;
     return R;
 }
 
@@ -692,24 +692,6 @@ __device__ __forceinline__ float key_bf(int k) {
     return __uint_as_float(b << 16);
 }
 
-// A value g such that at least c lanes of the wave have lmax >= g, by bisection between the wave's smallest and
-// largest finite lane maxima (-inf when fewer than c lanes hold a finite value).  Any element among the wave's c
-// largest is >= g: c lane maxima are >= g, and an element below g is exceeded by all of them.
-__device__ __forceinline__ float wave_gate(float lmax, int c) {
-    const bool fin = lmax > -INFINITY;
-    if (__popcll(ballot(fin)) < c) return -INFINITY;
-    float lo = wave_reduce(fin ? lmax : INFINITY, [](float a, float b) { return fminf(a, b); });
-    float hi = wave_reduce(fin ? lmax : -INFINITY, [](float a, float b) { return fmaxf(a, b); });
-    for (int it = 0; it < 10; ++it) {
-        const float mid = 0.5f * lo + 0.5f * hi;
-        if (!(mid > lo && mid < hi)) break;
-        if (__popcll(ballot(lmax >= mid)) >= c)
-            lo = mid;
-        else
-            hi = mid;
-    }
-    return lo;
-}
 
 enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2 };
 
@@ -763,6 +745,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         L.scnt = 0;
     }
     if (tid < kMaxSB) L.sbfx[tid] = 0ull;
+    if (tid < 256) L.gh[tid] = 0u;
     __syncthreads();
     // the history: counts and first occurrences (specials); a censored EOS is taken out of the tile (and listed as a
     // special when it ranks but is not drawn)
@@ -883,12 +866,8 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         return arrive(A, R, L) ? kActFinalize : kActNone;
     }
 
-    // top-k and top-p rows: each wave's gate (c lane maxima at or above it); the slice publishes every element at or
-    // above the highest of them (the finaliser needs its cut at or above the highest gate of the row anyway, so
-    // elements below it are never used), folded into the maxima's reduction
     const bool gated = R.mode == kTopK || R.mode == kNucleus;
-    const float wgate = gated ? wave_gate(lmax, R.c_gate) : -INFINITY;
-    const float4 mx = block_max4(make_float4(lmax, smax, sdmax, wgate), L.red);
+    const float4 mx = block_max4(make_float4(lmax, smax, sdmax, (gated && lmax > -INFINITY) ? -lmax : -INFINITY), L.red);
     const float tmq = is_finite_f(mx.x) ? to_q<ES>(R, mx.x) : mx.x;  // tile max, processed domain
     const float mq = fmaxf(tmq, mx.y);
     const float mqd = fmaxf(tmq, mx.z);
@@ -938,7 +917,30 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     }
 
     // top-k and top-p rows: per-wave gates; every element of the wave at or above its gate is published
-    const float gate = mx.w;  // the slice's gate, in the tile's domain
+    // the slice's gate (tile domain): a value that at least c_gate of its lane maxima reach, the c-th largest lane max
+    // to within one bin of a 256-bin histogram of them over [min, max]; each wave reads the histogram itself
+    const float hi_l = mx.x, lo_l = -mx.w;
+    const float span_l = hi_l - lo_l;
+    const bool binned = span_l > 1e-6f * fmaxf(1.0f, fabsf(hi_l));
+    const float scale_l = binned ? 256.0f / span_l : 0.0f;
+    if (lmax > -INFINITY) atomicAdd(&L.gh[binned ? min(255, (int)((lmax - lo_l) * scale_l)) : 0], 1u);
+    __syncthreads();
+    float gate = -INFINITY;
+    {
+        const uint4 hv = *(const uint4*)&L.gh[252 - 4 * l];  // bins 255 - 4l .. 252 - 4l, from the top
+        const int v0 = (int)hv.w, v1 = (int)hv.z, v2 = (int)hv.y, v3 = (int)hv.x;
+        const int sum = v0 + v1 + v2 + v3;
+        const int incl = wave_incl_scan(sum);
+        const int c = R.c_gate;
+        if (__builtin_amdgcn_readlane(incl, 63) >= c) {
+            const int ex = incl - sum;
+            const int ls = __ffsll((long long)ballot(ex < c && c <= incl)) - 1;
+            const int t = ex + v0 >= c ? 0 : (ex + v0 + v1 >= c ? 1 : (ex + v0 + v1 + v2 >= c ? 2 : 3));
+            const int b = 255 - (4 * ls + __builtin_amdgcn_readlane(t, ls));
+            // one bin lower than the bin reached, so rounding in the binning cannot put a counted lane below it
+            gate = (!binned || b <= 0) ? lo_l : lo_l + (float)(b - 1) * (span_l * (1.0f / 256.0f));
+        }
+    }
     const float gate_q = (gate > -INFINITY) ? to_q<ES>(R, gate) : -INFINITY;
     unsigned long long* segs = (unsigned long long*)((char*)rec + kRecCandOff);
     unsigned long long* myseg = segs + (int64_t)w * kCapWave;
@@ -1819,6 +1821,189 @@ __device__ __forceinline__ bool wselect_draw(const Row& R, Lds& L, WSet s, float
     return true;
 }
 
+// ------------------------------------------------------------------ small candidate sets: sorted in registers
+//
+// Up to 256 candidates: one bitonic sort by (value descending, index) puts them in rank order, after which the k-th
+// value, the top-p cut and min_keep are rank lookups and one prefix scan; a second sort by token id (the id and
+// the mass packed in one 64-bit key) gives the draw.  No LDS round trips between the steps.
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long x, int j) {
+    switch (j) {
+    case 1: return shfl_xor<1>(x);
+    case 2: return shfl_xor<2>(x);
+    case 4: return shfl_xor<4>(x);
+    case 8: return shfl_xor<8>(x);
+    case 16: return shfl_xor<16>(x);
+    default: return shfl_xor<32>(x);
+    }
+}
+
+// v[p] is element p * 64 + lane of a bitonic network over 64 P keys; sorted ascending on return.
+template <int P>
+__device__ __forceinline__ void wave_bitonic(unsigned long long (&v)[P]) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int k = 2; k <= 64 * P; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            unsigned long long w[P];
+#pragma unroll
+            for (int p = 0; p < P; ++p) w[p] = j >= 64 ? v[p ^ (j >> 6)] : shfl_xor_u64(v[p], j);
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+                const int i = p * 64 + lane;
+                const bool keep_min = ((i & j) == 0) == ((i & k) == 0);
+                const bool lt = v[p] < w[p];
+                v[p] = (lt == keep_min) ? v[p] : w[p];
+            }
+        }
+    }
+}
+
+// The value of x[] at rank r (uniform r < 64 P): element r of the rank order.
+template <int P, class T>
+__device__ __forceinline__ T at_rank(const T (&x)[P], int r) {
+    T y = x[0];
+#pragma unroll
+    for (int p = 1; p < P; ++p)
+        if ((r >> 6) == p) y = x[p];
+    if constexpr (sizeof(T) == 8) return (T)readlane_u64((unsigned long long)y, r & 63);
+    else return (T)__builtin_amdgcn_readlane((int)y, r & 63);
+}
+
+// select_draw for at most 64 P candidates (n >= 1), on wave 0.
+template <int P>
+__device__ __forceinline__ bool wsort_select_draw(const Row& R, const WSet& s, float m_sel, double zfull_fx, float gate,
+                                                  bool all_gate_inf, float u, Outcome& out) {
+    const int l = lane_id();
+    const int n = s.n;
+    unsigned long long v[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int i = p * 64 + l;
+        const float q = s.q[min(i, n - 1)];
+        v[p] = i < n ? (((unsigned long long)~ord_key(q) << 32) | (uint32_t)i) : ~0ull;
+    }
+    wave_bitonic<P>(v);
+    uint32_t key[P], id[P];
+    unsigned long long mass[P];
+    bool valid[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int r = p * 64 + l;
+        valid[p] = r < n;
+        const int ix = valid[p] ? (int)(uint32_t)v[p] : 0;
+        key[p] = ~(uint32_t)(v[p] >> 32);
+        id[p] = s.id[ix];
+        mass[p] = s.mass[ix];
+    }
+    const bool topk = R.kk < R.V;
+    float kth = -INFINITY;
+    unsigned long long cnt_gt = (unsigned long long)n;
+    if (topk) {
+        if (R.kk <= n) {
+            kth = key_float(at_rank<P>(key, R.kk - 1));
+            const uint32_t kk_key = ord_key(kth);
+            cnt_gt = 0ull;
+#pragma unroll
+            for (int p = 0; p < P; ++p) cnt_gt += (unsigned long long)__popcll(ballot(valid[p] && key[p] > kk_key));
+            if (!(kth >= gate)) return false;
+        } else if (!all_gate_inf) {
+            return false;
+        }
+    }
+    const uint32_t kthkey = ord_key(kth);
+    float thr = kth;
+    if (R.p_active) {
+        const unsigned long long ekth = efx(kth, m_sel);
+        const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
+        unsigned long long wr[P];
+        unsigned long long above = 0ull;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            wr[p] = (valid[p] && key[p] > kthkey) ? mass[p] : 0ull;
+            above += wr[p];
+            if ((unsigned long long)(p * 64 + l) == cnt_gt) wr[p] += vw;  // the ties at kth, at its first rank
+        }
+        double zn;
+        if (topk && !R.hf)
+            zn = (double)(wave_sum(above) + vw);
+        else
+            zn = zfull_fx;
+        const double pt = ceil((double)R.top_p * zn);
+        const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+        int rcut = -1;
+        unsigned long long carry = 0ull;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const unsigned long long incl = wave_incl_scan(wr[p]) + carry;
+            const uint64_t hit = ballot(incl >= T);
+            if (rcut < 0 && hit) rcut = p * 64 + __ffsll((long long)hit) - 1;
+            carry = readlane_u64(incl, 63);
+        }
+        float thr_p;
+        if (rcut >= 0) {
+            thr_p = key_float(at_rank<P>(key, rcut));
+        } else {
+            if (!topk) return false;  // the nucleus reaches below the candidates
+            thr_p = kth;
+        }
+        if (!topk && !(thr_p >= gate)) return false;
+        float vmk = m_sel;
+        if (R.min_keep_eff >= 2) {
+            if (R.min_keep_eff > n) {
+                vmk = -INFINITY;
+            } else {
+                vmk = key_float(at_rank<P>(key, R.min_keep_eff - 1));
+                if (!(vmk >= gate)) return false;
+            }
+        }
+        thr = fminf(thr_p, vmk);
+        if (topk) thr = fmaxf(thr, kth);
+    }
+    // survivors: drawable, q >= thr; the first in rank order is the largest
+    const uint32_t thrkey = ord_key(thr);
+    bool surv[P];
+    int first = -1;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        surv[p] = valid[p] && key[p] >= thrkey && !(id[p] & kSelOnlyBit);  // candidates are finite
+        const uint64_t b = ballot(surv[p]);
+        if (first < 0 && b) first = p * 64 + __ffsll((long long)b) - 1;
+    }
+    const float md = first >= 0 ? key_float(at_rank<P>(key, first)) : -INFINITY;
+    out.thr = thr;
+    out.mdraw = md;
+    out.token = R.V - 1;
+    if (!(md > -INFINITY)) return true;
+    const bool md_is_m = md == m_sel;
+    unsigned long long zs = 0ull;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const unsigned long long m2 = surv[p] ? (md_is_m ? mass[p] : efx(key_float(key[p]), md)) : 0ull;
+        zs += m2;
+        v[p] = surv[p] ? (((unsigned long long)(id[p] & ~kSelOnlyBit) << 43) | m2) : ~0ull;  // id < 2^21, mass < 2^43
+    }
+    zs = wave_sum(zs);
+    if (zs == 0ull) return true;
+    const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
+    wave_bitonic<P>(v);  // survivors by token id
+    constexpr unsigned long long kMassMask = (1ull << 43) - 1ull;
+    unsigned long long carry = 0ull;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const unsigned long long w = v[p] == ~0ull ? 0ull : (v[p] & kMassMask);
+        const unsigned long long incl = wave_incl_scan(w) + carry;
+        const uint64_t hit = ballot(v[p] != ~0ull && incl >= T2);
+        if (hit) {
+            out.token = (int64_t)(readlane_u64(v[p], __ffsll((long long)hit) - 1) >> 43);
+            return true;
+        }
+        carry = readlane_u64(incl, 63);
+    }
+    return true;
+}
+
 // Candidate rows: every slice's candidates gathered into LDS (the whole workgroup), then selected and drawn on
 // wave 0.  False: the histogram path or streaming instead.
 __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
@@ -1915,8 +2100,18 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
         const uint32_t klo = n ? (uint32_t)L.uscratch[0] : 0u, khi = n ? (uint32_t)L.uscratch[1] : 0u;
         Outcome o;
-        const bool ok = wselect_draw(R, L, s, m_sel, L.dscratch[0] * kFx, L.fscratch[1], L.is_last == 0, klo, khi,
-                                     L.fscratch[2], o);
+        const double zf = L.dscratch[0] * kFx;
+        const float gate = L.fscratch[1], u = L.fscratch[2];
+        const bool ginf = L.is_last == 0;
+        bool ok;
+        if (n >= 1 && n <= 64)
+            ok = wsort_select_draw<1>(R, s, m_sel, zf, gate, ginf, u, o);
+        else if (n >= 1 && n <= 128)
+            ok = wsort_select_draw<2>(R, s, m_sel, zf, gate, ginf, u, o);
+        else if (n >= 1 && n <= 256)
+            ok = wsort_select_draw<4>(R, s, m_sel, zf, gate, ginf, u, o);
+        else
+            ok = wselect_draw(R, L, s, m_sel, zf, gate, ginf, klo, khi, u, o);
         if (l == 0) {
             L.token = ok ? 1 : 0;
             L.fscratch[3] = o.thr;
