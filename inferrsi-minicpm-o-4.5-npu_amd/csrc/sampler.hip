@@ -1581,6 +1581,9 @@ __device__ __forceinline__ T wave_sum(T x) {
     return wave_reduce(x, [](T a, T b) { return a + b; });
 }
 
+__device__ __forceinline__ int scan_bins256(const unsigned long long* bins, bool desc, unsigned long long T,
+                                            unsigned long long& before);
+
 // One round of a wave selection: 256 bins, lane l holding bins 4l .. 4l + 3 (scan order: descending visits bins
 // 255 .. 0, ascending 0 .. 255; bins past the range are empty).  Returns the bin where the cumulative weight
 // reaches T and the weight before it, or -1 when the total is below T.
@@ -1611,6 +1614,17 @@ __device__ __forceinline__ int wround(const WSet& s, const WSel& P, bool desc, u
     }
     if (l == 0 && vw && vkey >= klo && vkey <= khi) atomicAdd(&bins[bin_of(vkey, key_float(vkey))], vw);
     wave_lds_sync();
+    const int b = scan_bins256(bins, desc, T, before);
+    wave_lds_sync();  // read before the next round clears them
+    return b;
+}
+
+// The bin of 256 (lane l reads bins 4l .. 4l + 3) where the cumulative weight in scan order (descending: bins
+// 255 .. 0) reaches T, and the weight before it; -1 when the total is below T.  One wave, no synchronisation.
+__device__ __forceinline__ int scan_bins256(const unsigned long long* bins, bool desc, unsigned long long T,
+                                            unsigned long long& before) {
+    const int l = lane_id();
+    const ulonglong2* bins2 = (const ulonglong2*)bins;
     unsigned long long v[4];
     if (desc) {
         const ulonglong2 hi = bins2[127 - 2 * l], lo = bins2[126 - 2 * l];
@@ -1625,7 +1639,6 @@ __device__ __forceinline__ int wround(const WSet& s, const WSel& P, bool desc, u
         v[2] = b.x;
         v[3] = b.y;
     }
-    wave_lds_sync();  // read before the next round clears them
     const unsigned long long sum = v[0] + v[1] + v[2] + v[3];
     const unsigned long long incl = wave_incl_scan(sum);
     if (readlane_u64(incl, 63) < T) return -1;
@@ -2004,6 +2017,260 @@ __device__ __forceinline__ bool wsort_select_draw(const Row& R, const WSet& s, f
     return true;
 }
 
+// The draw over a set of survivors (drawable, q >= thr; 1 <= n <= 64 P) on wave 0: md, their masses relative to
+// it, and the inverse CDF in token order after a sort by id.
+template <int P>
+__device__ __forceinline__ void wsurv_draw(const WSet& sv, float m_sel, float u, Outcome& out) {
+    const int l = lane_id();
+    const int n = sv.n;
+    float q[P];
+    uint32_t id[P];
+    unsigned long long m[P];
+    float md = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const int i = p * 64 + l, ic = min(i, n - 1);
+        q[p] = i < n ? sv.q[ic] : -INFINITY;
+        id[p] = sv.id[ic];
+        m[p] = sv.mass[ic];
+        md = fmaxf(md, q[p]);
+    }
+    md = wave_reduce(md, [](float a, float b) { return fmaxf(a, b); });
+    out.mdraw = md;
+    const bool md_is_m = md == m_sel;
+    unsigned long long zs = 0ull, v[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const bool in = q[p] > -INFINITY;
+        const unsigned long long m2 = in ? (md_is_m ? m[p] : efx(q[p], md)) : 0ull;
+        zs += m2;
+        v[p] = in ? (((unsigned long long)(id[p] & ~kSelOnlyBit) << 43) | m2) : ~0ull;
+    }
+    zs = wave_sum(zs);
+    if (zs == 0ull) return;
+    const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
+    wave_bitonic<P>(v);
+    unsigned long long carry = 0ull;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+        const unsigned long long w = v[p] == ~0ull ? 0ull : (v[p] & ((1ull << 43) - 1ull));
+        const unsigned long long incl = wave_incl_scan(w) + carry;
+        const uint64_t hit = ballot(v[p] != ~0ull && incl >= T2);
+        if (hit) {
+            out.token = (int64_t)(readlane_u64(v[p], __ffsll((long long)hit) - 1) >> 43);
+            return;
+        }
+        carry = readlane_u64(incl, 63);
+    }
+}
+
+// range_find over a large candidate set by the whole workgroup (every thread calls it).  Rounds of 256 bins, the
+// first by value (then later rounds keep only that bin's entries), the rest by key; each round takes one barrier:
+// every wave scans the bins itself, and the bins of consecutive rounds rotate over three buffers, so that a buffer
+// is cleared only once every wave has scanned it.
+__device__ __forceinline__ bool bsel(const WSet& s, const WSel& P, bool desc, unsigned long long T, uint32_t klo,
+                                     uint32_t khi, uint32_t vkey, unsigned long long vw, Lds& L, uint32_t& key_out,
+                                     unsigned long long& before_out) {
+    const int tid = threadIdx.x;
+    unsigned long long* buf = L.h.w;  // 3 x 256 bins
+    __syncthreads();                   // the previous selection's scans are done
+    if (tid < 256) buf[tid] = 0ull;
+    __syncthreads();
+    float qlo = 0.0f, scale = 0.0f;
+    bool value_round = false;
+    if (P.sel != kSelDraw && khi > klo) {
+        qlo = key_float(klo);
+        scale = 256.0f / (key_float(khi) - qlo);
+        value_round = scale > 0.0f && scale < INFINITY;
+    }
+    auto vbin = [&](float q) { return min(255, (int)((q - qlo) * scale)); };
+    int vsel = -1;  // after the value round: the bin every counted entry must fall in
+    unsigned long long acc = 0ull;
+    for (int r = 0;; ++r) {
+        unsigned long long* cur = buf + 256 * (r % 3);
+        unsigned long long* nxt = buf + 256 * ((r + 1) % 3);
+        int sh = 0;
+        if (!value_round) {
+            const uint64_t span = (uint64_t)khi - klo + 1;
+            while (((span - 1) >> sh) >= 256ull) ++sh;
+        }
+        for (int i = tid; i < s.n; i += kThreads) {
+            uint32_t key;
+            unsigned long long w;
+            wentry(s, i, P, key, w);
+            const float q = s.q[i];
+            const bool in = w && key >= klo && key <= khi && (vsel < 0 || vbin(q) == vsel);
+            if (in) atomicAdd(&cur[value_round ? vbin(q) : (int)((key - klo) >> sh)], w);
+        }
+        if (tid == 0 && vw && vkey >= klo && vkey <= khi) {
+            const float vq = key_float(vkey);
+            if (vsel < 0 || vbin(vq) == vsel) atomicAdd(&cur[value_round ? vbin(vq) : (int)((vkey - klo) >> sh)], vw);
+        }
+        if (tid < 256) nxt[tid] = 0ull;
+        __syncthreads();
+        unsigned long long bef = 0ull;
+        const int b = scan_bins256(cur, desc, T, bef);
+        if (b < 0) return false;
+        T -= bef;
+        acc += bef;
+        if (value_round) {
+            // keys of the bin's values, widened by a bin on each side (membership is tested by the bin itself)
+            vsel = b;
+            value_round = false;
+            const uint32_t a = ord_key(qlo + (float)(b - 1) / scale), z = ord_key(qlo + (float)(b + 2) / scale);
+            klo = max(klo, a);
+            khi = min(khi, z);
+            continue;
+        }
+        const uint64_t a = (uint64_t)klo + ((uint64_t)b << sh);
+        klo = (uint32_t)a;
+        khi = (uint32_t)std::min<uint64_t>((uint64_t)khi, a + (1ull << sh) - 1);
+        if (sh == 0) break;
+    }
+    key_out = klo;
+    before_out = acc;
+    return true;
+}
+
+// select_draw for a large candidate set by the whole workgroup (every thread calls it; the result is in out on
+// every thread).  The survivors are compacted; up to 256 of them are drawn by wave 0 with a sort.
+__device__ __forceinline__ bool bselect_draw(const Row& R, Lds& L, const WSet& s, float m_sel, double zfull_fx,
+                                             float gate, bool all_gate_inf, uint32_t klo, uint32_t khi, float u,
+                                             Outcome& out) {
+    const int tid = threadIdx.x;
+    const int n_fin = s.n;
+    const bool topk = R.kk < R.V;
+    WSel P;
+    P.kth = P.thr = P.md = -INFINITY;
+    P.md_is_m = true;
+    float kth = -INFINITY;
+    unsigned long long cnt_gt = (unsigned long long)n_fin;
+    uint32_t key = 0u;
+    unsigned long long bf = 0ull;
+    if (topk) {
+        if ((unsigned long long)R.kk <= (unsigned long long)n_fin) {
+            P.sel = kSelCount;
+            bsel(s, P, true, (unsigned long long)R.kk, klo, khi, 0u, 0ull, L, key, bf);
+            kth = key_float(key);
+            cnt_gt = bf;
+            if (!(kth >= gate)) return false;
+            klo = key;
+        } else if (!all_gate_inf) {
+            return false;
+        }
+    }
+    float thr = kth;
+    if (R.p_active) {
+        P.kth = kth;
+        const unsigned long long ekth = efx(kth, m_sel);
+        const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
+        double zn;
+        if (topk && !R.hf) {
+            unsigned long long a = 0ull;
+            for (int i = tid; i < s.n; i += kThreads) {
+                const float q = s.q[i];
+                const unsigned long long m = s.mass[i];
+                a += q > kth ? m : 0ull;
+            }
+            zn = (double)(block_sum_u(a, L.red) + vw);
+        } else {
+            zn = zfull_fx;
+        }
+        const double pt = ceil((double)R.top_p * zn);
+        const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+        const uint32_t kthkey = ord_key(kth);
+        P.sel = kSelCut;
+        const bool found = bsel(s, P, true, T, (kth > -INFINITY) ? max(klo, kthkey) : klo, khi, kthkey, vw, L, key, bf);
+        float thr_p;
+        if (found) {
+            thr_p = key_float(key);
+        } else {
+            if (!topk) return false;
+            thr_p = kth;
+        }
+        if (!topk && !(thr_p >= gate)) return false;
+        float vmk = m_sel;
+        if (R.min_keep_eff >= 2) {
+            if ((unsigned long long)R.min_keep_eff > (unsigned long long)n_fin) {
+                vmk = -INFINITY;
+            } else {
+                P.sel = kSelCount;
+                bsel(s, P, true, (unsigned long long)R.min_keep_eff, klo, khi, 0u, 0ull, L, key, bf);
+                vmk = key_float(key);
+                if (!(vmk >= gate)) return false;
+            }
+        }
+        thr = fminf(thr_p, vmk);
+        if (topk) thr = fmaxf(thr, kth);
+    }
+    // survivors: drawable, q >= thr, compacted into L.sm[0] when they fit
+    if (tid == 0) L.scnt = 0;
+    __syncthreads();
+    SmallSet& d = L.sm[0];
+    for (int i0 = 0; i0 < s.n; i0 += kThreads) {
+        const int i = min(i0 + tid, s.n - 1);
+        const float q = s.q[i];
+        const uint32_t id = s.id[i];
+        const bool sv = i0 + tid < s.n && !(id & kSelOnlyBit) && q >= thr && q > -INFINITY;
+        const int slot = lds_reserve(sv, &L.scnt);
+        if (sv && slot < kCapSmall) {
+            d.q[slot] = q;
+            d.id[slot] = id;
+            d.mass[slot] = s.mass[i];
+        }
+    }
+    __syncthreads();
+    const int ns = L.scnt;
+    out.thr = thr;
+    out.mdraw = -INFINITY;
+    out.token = R.V - 1;
+    if (ns == 0) return true;
+    if (ns <= 256) {
+        const WSet sv = wset_of(d.q, d.id, d.mass, ns);
+        if (wave_id() == 0) {
+            Outcome o = out;
+            if (ns <= 64)
+                wsurv_draw<1>(sv, m_sel, u, o);
+            else if (ns <= 128)
+                wsurv_draw<2>(sv, m_sel, u, o);
+            else
+                wsurv_draw<4>(sv, m_sel, u, o);
+            if (lane_id() == 0) {
+                L.fscratch[3] = o.mdraw;
+                L.uscratch[1] = (unsigned long long)o.token;
+            }
+        }
+        __syncthreads();
+        out.mdraw = L.fscratch[3];
+        out.token = (int64_t)L.uscratch[1];
+        return true;
+    }
+    // many survivors: the block finds md, their sum and the draw over the whole set
+    float md = -INFINITY;
+    for (int i = tid; i < s.n; i += kThreads) {
+        const float q = s.q[i];
+        const uint32_t id = s.id[i];
+        if (!(id & kSelOnlyBit) && q >= thr) md = fmaxf(md, q);
+    }
+    md = block_max_f(md, L.red);
+    out.mdraw = md;
+    P.sel = kSelDraw;
+    P.thr = thr;
+    P.md = md;
+    P.md_is_m = md == m_sel;
+    unsigned long long zs = 0ull;
+    for (int i = tid; i < s.n; i += kThreads) {
+        uint32_t k;
+        unsigned long long w;
+        wentry(s, i, P, k, w);
+        zs += w;
+    }
+    zs = block_sum_u(zs, L.red);
+    const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
+    if (zs > 0ull && bsel(s, P, false, T2, 0u, (uint32_t)(R.V - 1), 0u, 0ull, L, key, bf)) out.token = (int64_t)key;
+    return true;
+}
+
 // Candidate rows: every slice's candidates gathered into LDS (the whole workgroup), then selected and drawn on
 // wave 0.  False: the histogram path or streaming instead.
 __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
@@ -2096,9 +2363,14 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         atomicMax((unsigned long long*)&L.uscratch[1], (unsigned long long)kmax);
     }
     __syncthreads();
+    const uint32_t klo = n ? (uint32_t)L.uscratch[0] : 0u, khi = n ? (uint32_t)L.uscratch[1] : 0u;
+    if (n > 256) {  // a large set: the whole workgroup selects
+        const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
+        return bselect_draw(R, L, s, m_sel, L.dscratch[0] * kFx, L.fscratch[1], L.is_last == 0, klo, khi,
+                            L.fscratch[2], out);
+    }
     if (w == 0) {
         const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
-        const uint32_t klo = n ? (uint32_t)L.uscratch[0] : 0u, khi = n ? (uint32_t)L.uscratch[1] : 0u;
         Outcome o;
         const double zf = L.dscratch[0] * kFx;
         const float gate = L.fscratch[1], u = L.fscratch[2];
@@ -2108,7 +2380,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
             ok = wsort_select_draw<1>(R, s, m_sel, zf, gate, ginf, u, o);
         else if (n >= 1 && n <= 128)
             ok = wsort_select_draw<2>(R, s, m_sel, zf, gate, ginf, u, o);
-        else if (n >= 1 && n <= 256)
+        else if (n >= 1)
             ok = wsort_select_draw<4>(R, s, m_sel, zf, gate, ginf, u, o);
         else
             ok = wselect_draw(R, L, s, m_sel, zf, gate, ginf, klo, khi, u, o);
