@@ -160,10 +160,13 @@ def _cfg_group(logits: torch.Tensor, history: torch.Tensor, steps: torch.Tensor,
                **kw) -> RowGroup:
     _check_semantics(cfg)
     dev = logits.device
+    # The reference forces EOS at steps >= max_new_tokens - 1 (:157), so max_new_tokens <= 0 forces it on every
+    # frame (frame indices are >= 0); the kernel reads 0 as "never", so such a budget is passed as 1.
+    max_new = int(cfg.max_new_tokens) if int(cfg.max_new_tokens) > 0 else 1
     return RowGroup(logits, temperature=float(cfg.temperature), top_k=int(cfg.top_k), top_p=float(cfg.top_p),
                     repetition=float(cfg.repetition_penalty), alpha_lut=_alpha_table(cfg.repetition_penalty, dev),
                     history=history, eos=int(eos), min_new_tokens=int(cfg.min_new_tokens),
-                    max_new_tokens=int(cfg.max_new_tokens), semantics=cfg.semantics,
+                    max_new_tokens=max_new, semantics=cfg.semantics,
                     min_keep=int(cfg.min_keep) if cfg.semantics == "hf" else 1, top_k_zero_disables=False,
                     top_p_one_disables=False, steps=steps, **kw)
 

@@ -1,9 +1,18 @@
 """Parity helpers shared by the GPU tests: oracle adapters and float-boundary classification.
 
-A token or support difference between the HIP path and the oracle is accepted
-only when the oracle's own float64 arithmetic puts the decision within a
-relative 1e-5 of its boundary (the inverse-CDF target lands on a CDF step, or
-a rank's exclusive mass is at top_p); every other difference fails.
+A token or support difference between the HIP path and the oracle is accepted only where the two computations'
+own rounding can move the decision, and the tolerance is derived per row, not fixed:
+
+* the oracle (the reference's arithmetic) forms its CDF, its draw target and its top-p exclusive masses in float32;
+  the classifier recomputes them exactly as the oracle does and measures their deviation from the float64 values
+  on that row (``oracle_dev``);
+* the HIP path forms each element's mass as exp(q - max) with the device ``expf`` (within 1 ulp) rounded to
+  2^-42 fixed point and sums exactly, so its CDF deviates from float64 by at most 2^-23 of the total
+  (``GPU_BOUND``).
+
+A difference passes only when the float64 CDF at every step between the two tokens (or the exclusive mass at the
+cut) lies within ``oracle_dev + GPU_BOUND`` of the decision point.  The workload tests additionally require that
+no row needs this allowance on their seeds.
 """
 
 from __future__ import annotations
@@ -13,7 +22,7 @@ import torch
 
 from oracle import extended_ref as ext
 
-BOUNDARY_TOL = 1e-5
+GPU_BOUND = 2.0 ** -23  # relative to the row's total mass
 
 
 def oracle_rows(wl, *, zero_disables=True, one_disables=True, alpha="exact", **over) -> ext.Rows:
@@ -29,19 +38,33 @@ def oracle_rows(wl, *, zero_disables=True, one_disables=True, alpha="exact", **o
     return ext.Rows(**kw)
 
 
-def token_at_boundary(x: torch.Tensor, u: float, a: int, b: int, tol: float = BOUNDARY_TOL) -> bool:
-    """Tokens a != b from the same processed row differ only by where u * total falls on a CDF step."""
+def draw_margin(x: torch.Tensor, u: float, a: int, b: int) -> tuple[float, float]:
+    """(distance, tolerance) of the decision between tokens a != b drawn from processed row x with uniform u:
+    the largest |cdf64[j] - u * total64| over the CDF steps j in [min(a, b), max(a, b)), relative to the total,
+    and the tolerance the two computations' rounding allows on this row."""
     x64 = x.double()
-    p = torch.softmax(x64, dim=-1)
-    cdf = torch.cumsum(p, dim=-1)
-    t = u * float(cdf[-1])
+    cdf64 = torch.cumsum(torch.softmax(x64, dim=-1), dim=-1)
+    tot64 = float(cdf64[-1])
+    t64 = u * tot64
+    cdf32 = torch.softmax(x.float()[None], dim=-1).cumsum(dim=-1)[0]  # the oracle's own arithmetic
+    t32 = float(torch.tensor(u, dtype=torch.float32) * cdf32[-1])
     lo, hi = min(a, b), max(a, b)
-    return abs(float(cdf[lo]) - t) < tol and abs(float(cdf[hi - 1]) - t) < tol
+    dist = float((cdf64[lo:hi] - t64).abs().max()) / tot64
+    finite = torch.isfinite(x64)
+    oracle_dev = (float((cdf32.double() - cdf64)[finite].abs().max()) + abs(t32 - t64)) / tot64
+    return dist, oracle_dev + GPU_BOUND
+
+
+def token_at_boundary(x: torch.Tensor, u: float, a: int, b: int) -> bool:
+    """Tokens a != b from the same processed row differ only by where u * total falls on a CDF step."""
+    dist, tol = draw_margin(x, u, a, b)
+    return dist <= tol
 
 
 def support_at_boundary(pre: torch.Tensor, got: torch.Tensor, want: torch.Tensor, top_p: float, k: int,
-                        full_norm: bool, tol: float = BOUNDARY_TOL) -> bool:
-    """Supports (finite entries) differ only in ranks whose exclusive mass sits at top_p (float64)."""
+                        full_norm: bool) -> bool:
+    """Supports (finite entries) differ only in ranks whose exclusive mass sits at top_p within the rounding of
+    the oracle's float32 masses (measured on this row) plus ``GPU_BOUND``."""
     diff = torch.nonzero(torch.isfinite(got) != torch.isfinite(want)).flatten()
     if diff.numel() == 0:
         return True
@@ -51,6 +74,12 @@ def support_at_boundary(pre: torch.Tensor, got: torch.Tensor, want: torch.Tensor
     z = torch.logsumexp(x64, 0) if full_norm else torch.logsumexp(vals, 0)
     probs = torch.exp(vals - z)
     above = torch.cumsum(probs, 0) - probs
+    # the oracle's float32 exclusive masses (engine/talker_sampler.py:111-115, :127-132)
+    v32 = pre.float()[order][:k]
+    p32 = torch.exp(v32 - torch.logsumexp(pre.float(), 0)) if full_norm else torch.softmax(v32, 0)
+    a32 = torch.cumsum(p32, 0) - p32
+    fin = torch.isfinite(above) & torch.isfinite(a32.double())
+    tol = float((a32.double() - above)[fin].abs().max()) + GPU_BOUND if bool(fin.any()) else GPU_BOUND
     rank = torch.empty_like(order)
     rank[order] = torch.arange(order.numel())
     for j in diff.tolist():
@@ -59,14 +88,16 @@ def support_at_boundary(pre: torch.Tensor, got: torch.Tensor, want: torch.Tensor
         # every rank holding this value (ties) is a candidate position of the boundary
         tied = torch.nonzero(vals == v).flatten()
         cands = tied.tolist() if tied.numel() else [r]
-        if not any(abs(float(above[c]) - top_p) < tol for c in cands if c < k):
+        if not any(abs(float(above[c]) - top_p) <= tol for c in cands if c < k):
             return False
     return True
 
 
 def compare_group(name, got_tokens, got_proc, got_probs, ref: dict, rows: ext.Rows, prob_rtol: float) -> dict:
-    """Asserts parity of one group; returns counts of exact and boundary-classified rows."""
+    """Asserts parity of one group; returns counts of exact and boundary-classified rows, and for each of the
+    latter its row, distance and tolerance (``boundary_rows``)."""
     n_exact = n_tok_boundary = n_sup_boundary = 0
+    notes = []
     toks = got_tokens.cpu()
     for i in range(rows.rows):
         want_x = ref["processed"][i]
@@ -82,6 +113,7 @@ def compare_group(name, got_tokens, got_proc, got_probs, ref: dict, rows: ext.Ro
                 sup_ok = support_at_boundary(pre, gx, want_x, float(rows.top_p[i]), k, rows.semantics == "hf")
                 assert sup_ok, f"{name} row {i}: support differs away from the top-p boundary"
                 n_sup_boundary += 1
+                notes.append(f"row {i}: support at the top-p cut")
             both = torch.isfinite(gx) & torch.isfinite(want_x)
             assert torch.equal(gx[both], want_x[both]), f"{name} row {i}: processed values differ"
         if got_probs is not None and got_proc is not None and torch.equal(torch.isfinite(got_proc[i].cpu()),
@@ -93,12 +125,15 @@ def compare_group(name, got_tokens, got_proc, got_probs, ref: dict, rows: ext.Ro
         if got_t != want_t:
             x = got_proc[i].cpu() if got_proc is not None else want_x
             assert got_t >= 0 and want_t >= 0, f"{name} row {i}: PAD mismatch {got_t} vs {want_t}"
-            assert token_at_boundary(x, float(ref["uniforms"][i]), got_t, want_t), \
-                f"{name} row {i}: token {got_t} vs oracle {want_t} away from a CDF boundary"
+            dist, tol = draw_margin(x, float(ref["uniforms"][i]), got_t, want_t)
+            assert dist <= tol, (f"{name} row {i}: token {got_t} vs oracle {want_t} away from a CDF boundary "
+                                 f"(distance {dist:.3g} of the total, tolerance {tol:.3g})")
             n_tok_boundary += 1
+            notes.append(f"row {i}: token {got_t} vs {want_t}, distance {dist:.3g} <= {tol:.3g}")
         else:
             n_exact += 1
-    return {"exact": n_exact, "token_boundary": n_tok_boundary, "support_boundary": n_sup_boundary}
+    return {"exact": n_exact, "token_boundary": n_tok_boundary, "support_boundary": n_sup_boundary,
+            "boundary_rows": notes}
 
 
 def _prefilter(rows: ext.Rows, i: int) -> torch.Tensor:

@@ -2,9 +2,10 @@
 
 Every test runs the kernel on ``cuda:0`` and checks it against the CPU oracle
 on the same seeded inputs: tokens bit-exact (a difference is accepted only
-when the oracle's float64 arithmetic puts it within 1e-5 of a CDF or top-p
-boundary), processed logits bit-exact wherever both are finite, filtered
-probabilities within 1e-5 relative.
+where the float64 CDF or top-p mass sits within the two computations' own
+rounding of the decision point, measured per row, see ``tests/parity.py``;
+the workload tests allow none), processed logits bit-exact wherever both are
+finite, filtered probabilities within 1e-5 relative (fp32) / 2e-3 (bf16).
 """
 
 from __future__ import annotations
@@ -65,7 +66,8 @@ def test_workload_matches_oracle(name, make):
     stats = compare_group(name, g.tokens, g.processed, g.probs, ref, rows,
                           prob_rtol=1e-5 if wl.logits.dtype == torch.float32 else 2e-3)
     print(f"[gpu] {name}: {stats} paths {paths}", flush=True)
-    assert stats["exact"] >= wl.rows - max(1, wl.rows // 16)
+    # on these seeds no row may need the rounding allowance: every token and support is exact
+    assert stats["token_boundary"] == 0 and stats["support_boundary"] == 0, f"{name}: {stats['boundary_rows']}"
     assert paths["stream"] == 0 and sum(paths.values()) == wl.rows
 
 
@@ -87,7 +89,7 @@ def test_streaming_finalise_matches_oracle(name, make):
     stats = compare_group(name, g.tokens, g.processed, g.probs, ref, rows,
                           prob_rtol=1e-5 if wl.logits.dtype == torch.float32 else 2e-3)
     print(f"[gpu] streaming {name}: {stats}", flush=True)
-    assert stats["exact"] >= wl.rows - max(1, wl.rows // 16)
+    assert stats["token_boundary"] == 0 and stats["support_boundary"] == 0, f"{name}: {stats['boundary_rows']}"
 
 
 @pytest.mark.parametrize("rows", [1, 3, 5, 9, 13])
@@ -378,3 +380,48 @@ def test_errors_are_loud():
                             torch.zeros(1, dtype=torch.long, device=DEV), 3, hs.TalkerSampling(semantics="x"))
     with pytest.raises(ValueError):
         G.sample(torch.zeros(2, 8, device=DEV), eos=9)  # eos outside the vocabulary
+
+
+@pytest.mark.parametrize("semantics", ["hf", "omni"])
+def test_censored_eos_as_row_max_greedy_and_sampled(semantics):
+    """EOS is the row maximum (by far) while step < min_new_tokens: greedy rows (T = 0) and sampled rows must never
+    return it, and a sampled row's draw must renormalise over the other survivors (no underflow against the
+    censored maximum), in both pipeline orders."""
+    print(f"[gpu] censored EOS as the row max, {semantics}", flush=True)
+    gen = torch.Generator().manual_seed(404)
+    rows = 6
+    x = torch.randn(rows, V, generator=gen)
+    x[:, EOS] = torch.tensor([150.0, 150.0, 40.0, 200.0, 150.0, 1e4])
+    temps = torch.tensor([0.0, 0.8, 0.8, 1.0, 0.0, 0.7])
+    one = lambda val, dt=torch.float32: torch.full((rows,), val, dtype=dt)  # noqa: E731
+    hist = torch.randint(0, V, (rows, 16), generator=gen, dtype=torch.int64)
+    steps = torch.tensor([1, 2, 3, 4, 5, 6], dtype=torch.int64)
+    mk = 3 if semantics == "hf" else 1
+    ref_rows = ext.Rows(logits=x, temperature=temps, top_k=torch.tensor([25, 25, 0, 25, 0, 0], dtype=torch.int32),
+                        top_p=torch.tensor([0.85, 0.85, 0.9, 1.0, 1.0, 1.0]), repetition=one(1.05),
+                        presence=one(0.0), frequency=one(0.0), history=hist, seeds=one(9, torch.int64),
+                        steps=steps, eos=EOS, min_new_tokens=50, semantics=semantics, min_keep=mk)
+    g = G.RowGroup(x.to(DEV), temperature=temps.to(DEV), top_k=ref_rows.top_k.to(DEV), top_p=ref_rows.top_p.to(DEV),
+                   repetition=1.05, history=hist.to(DEV), seeds=one(9, torch.int64).to(DEV), steps=steps.to(DEV),
+                   eos=EOS, min_new_tokens=50, semantics=semantics, min_keep=mk, processed=True, probs=True)
+    G.launch([g])
+    torch.cuda.synchronize()
+    ref = ext.sample_rows(ref_rows)
+    stats = compare_group(f"eos_censor_{semantics}", g.tokens, g.processed, g.probs, ref, ref_rows, prob_rtol=1e-5)
+    assert stats["token_boundary"] == 0, stats["boundary_rows"]
+    assert (g.tokens.cpu() != EOS).all()
+
+
+def test_mirror_max_new_tokens_zero_forces_eos_every_frame():
+    """engine/talker_sampler.py:157: steps >= max_new_tokens - 1 holds for every frame when max_new_tokens <= 0."""
+    gen = torch.Generator().manual_seed(405)
+    x = torch.randn(3, V, generator=gen)
+    hist = torch.full((3, 16), -1, dtype=torch.int64)
+    steps = torch.tensor([0, 7, 60], dtype=torch.int64)
+    for max_new in (0, -3):
+        for sem in ("hf", "omni"):
+            cfg = hs.TalkerSampling(semantics=sem, rng="counter", max_new_tokens=max_new, min_new_tokens=0)
+            rcfg = ts.TalkerSampling(semantics=sem, rng="counter", max_new_tokens=max_new, min_new_tokens=0)
+            got = hs.processed_logits(x.to(DEV), hist.to(DEV), steps.to(DEV), EOS, cfg).cpu()
+            want = ts.processed_logits(x, hist, steps, EOS, rcfg)
+            assert torch.equal(got, want), (max_new, sem)
