@@ -16,10 +16,23 @@ constexpr int kWaves = kThreads / 64;
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
-// A pointer into global memory as such: accesses compile to global (not flat) instructions.
+// A pointer into global memory as such: accesses through it compile to global instructions.  A flat access
+// would also count against the LDS wait counter, so every LDS wait after a flat load waits for that load too.
 template <class T>
-__device__ __forceinline__ T* gp(T* p) {
-    return (T*)(__attribute__((address_space(1))) T*)p;
+using gptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<T> gp(T* p) {
+    return (gptr<T>)p;
+}
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// 16 bytes from global address a (16-byte aligned).
+__device__ __forceinline__ uint4 ld_u4(uintptr_t a) {
+    const u32x4_t v = *(gptr<const u32x4_t>)a;
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ int4 ld_i4(const void* p) {
+    const u32x4_t v = *(gptr<const u32x4_t>)p;
+    return make_int4((int)v.x, (int)v.y, (int)v.z, (int)v.w);
 }
 
 // Row-uniform values into scalar registers.

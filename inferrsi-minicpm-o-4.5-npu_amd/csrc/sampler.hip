@@ -67,6 +67,7 @@ enum Mode : int { kSkip = 0, kForced, kGreedy, kTopK, kNucleus, kFull, kStream }
 enum EosRule : int { kEosNormal = 0, kEosExcluded, kEosSelOnly };
 enum : int32_t { kRecOverflow = 1, kRecGateInf = 2 };
 constexpr uint32_t kSelOnlyBit = 0x80000000u;  // candidate id flag: EOS that ranks but is not drawn
+constexpr int kBufferWord3 = 0x00020000;       // raw buffer descriptor, word 3 (gfx9 family: 32-bit data format)
 
 struct DevGroup {
     const char* logits;
@@ -224,7 +225,29 @@ struct Row {
     bool hf, greedy, filters, p_active, pen, live, want_out, needz;
 };
 
-__device__ __forceinline__ Row make_row(const DevGroup& G, int gi, int row, int slice) {
+// The row's parameters as loaded (a slice issues these loads before its tile's: loads return in order).
+struct RowIn {
+    int64_t step;
+    float t, p, rep, pres, freq;
+    int k;
+    bool act, fin;
+};
+
+__device__ __forceinline__ RowIn load_row_in(const DevGroup& G, int row) {
+    RowIn I;
+    I.step = G.steps ? gp(G.steps)[row] : 0;
+    I.t = G.temperature ? gp(G.temperature)[row] : G.t_val;
+    I.p = G.top_p ? gp(G.top_p)[row] : G.p_val;
+    I.rep = G.repetition ? gp(G.repetition)[row] : G.rep_val;
+    I.pres = G.presence ? gp(G.presence)[row] : G.pres_val;
+    I.freq = G.frequency ? gp(G.frequency)[row] : G.freq_val;
+    I.k = G.top_k ? gp(G.top_k)[row] : G.k_val;
+    I.act = G.active ? gp(G.active)[row] != 0 : true;
+    I.fin = G.finished ? gp(G.finished)[row] != 0 : false;
+    return I;
+}
+
+__device__ __forceinline__ Row make_row(const DevGroup& G, int gi, int row, int slice, const RowIn& I) {
     Row R;
     R.gi = gi;
     R.row = row;
@@ -234,15 +257,10 @@ __device__ __forceinline__ Row make_row(const DevGroup& G, int gi, int row, int 
     R.V = G.vocab;
     R.lo = slice * G.slice_len;
     R.hi = min(G.vocab, R.lo + G.slice_len);
-    const int64_t step = G.steps ? gp(G.steps)[row] : 0;
-    const float t = G.temperature ? gp(G.temperature)[row] : G.t_val;
-    const float p = G.top_p ? gp(G.top_p)[row] : G.p_val;
-    const float rep = G.repetition ? gp(G.repetition)[row] : G.rep_val;
-    const float pres = G.presence ? gp(G.presence)[row] : G.pres_val;
-    const float freq = G.frequency ? gp(G.frequency)[row] : G.freq_val;
-    const int k = G.top_k ? gp(G.top_k)[row] : G.k_val;
-    const bool act = G.active ? gp(G.active)[row] != 0 : true;
-    const bool fin = G.finished ? gp(G.finished)[row] != 0 : false;
+    const int64_t step = I.step;
+    const float t = I.t, p = I.p, rep = I.rep, pres = I.pres, freq = I.freq;
+    const int k = I.k;
+    const bool act = I.act, fin = I.fin;
     R.step = uni(step);
     R.greedy = !(uni(t) > 0.f);
     R.T = R.greedy ? 1.0f : uni(t);
@@ -351,7 +369,7 @@ __device__ __forceinline__ const char* hist_row(const DevGroup& G, int row) {
 __device__ __forceinline__ void build_keep(const DevGroup& G, int row, int first, int len, int lo, int hi, Lds& L) {
     const int jb = (first >> 5) << 5;
     const int nw_row = (G.vocab + 31) >> 5;
-    const uint32_t* mrow = G.allowed ? gp(G.allowed) + (int64_t)row * G.allowed_stride : nullptr;
+    const gptr<const uint32_t> mrow = G.allowed ? gp(G.allowed) + (int64_t)row * G.allowed_stride : nullptr;
     const int nkw = min(kKeepWords, ((first + len - jb) + 31) / 32 + 1);
     for (int k = threadIdx.x; k < kKeepWords; k += kThreads) {
         uint32_t w = 0u;
@@ -389,7 +407,7 @@ __device__ __forceinline__ void build_counts(const DevGroup& G, const Row& R, in
     for (int b = 0; b < W; b += kThreads * 4) {
         int64_t h[4];
         if (!G.hist_i64 && (((uintptr_t)hrow & 15) == 0) && b + 4 * kThreads <= W) {
-            const int4 v = gp((const int4*)hrow)[(b >> 2) + threadIdx.x];
+            const int4 v = ld_i4((const int4*)hrow + (b >> 2) + threadIdx.x);
             h[0] = v.x;
             h[1] = v.y;
             h[2] = v.z;
@@ -491,6 +509,9 @@ struct Geo {
     uintptr_t base;   // 16-byte aligned address at or below element lo
     int first;        // element index at base (may be < lo)
     uintptr_t row_end;
+    // a raw buffer over [base, the row's end rounded up to 16 bytes): every chunk is wholly inside or wholly
+    // outside it, and a load outside returns zeros without a memory access
+    __amdgpu_buffer_rsrc_t rsrc;
 };
 
 template <int ES>
@@ -501,28 +522,21 @@ __device__ __forceinline__ Geo<ES> slice_geo(const DevGroup& G, int row, int lo)
     g.base = lo_addr & ~(uintptr_t)15;
     g.first = lo - (int)((lo_addr - g.base) / ES);
     g.row_end = (uintptr_t)(g.rowp + (int64_t)G.vocab * ES);
+    const uint32_t span = (uint32_t)(((g.row_end + 15) & ~(uintptr_t)15) - g.base);
+    g.rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)g.base, (short)0, (int)span, kBufferWord3);
     return g;
 }
 
-// Chunk c of the slice: 16 bytes at base + 16 c, elements first + E c + e.  Bytes outside the row are not read.
+// Chunk c of the slice: the 16 bytes at base + 16 c, elements first + E c + e; zeros for a chunk that starts at
+// or past element hi.  The bytes read outside the row (before its first element, after its last) share a 16-byte
+// block, and so a page, with an element of the row; the caller's range bits discard them.  No branches: the
+// loads of a tile are issued back to back and counted in order.
 template <int ES>
 __device__ __forceinline__ uint4 load_chunk(const Geo<ES>& g, int c, int hi) {
-    const uintptr_t a = g.base + (uintptr_t)c * 16;
     const int j0 = g.first + c * Geo<ES>::E;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (j0 >= hi) return v;
-    if (a >= (uintptr_t)g.rowp && a + 16 <= g.row_end) return *gp((const uint4*)a);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int e = 0; e < Geo<ES>::E; ++e) {
-        const uintptr_t ea = a + (uintptr_t)e * ES;
-        if (ea < (uintptr_t)g.rowp || ea + ES > g.row_end) continue;
-        if (ES == 2)
-            w[e >> 1] |= (uint32_t)*gp((const uint16_t*)ea) << (16 * (e & 1));
-        else
-            w[e] = *gp((const uint32_t*)ea);
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
+    const int off = j0 < hi ? c * 16 : 0x7ffffff0;  // out of the buffer's range: no access, zeros
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(g.rsrc, off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 // The keep bits of chunk c (E bits, element e at bit e).
@@ -544,7 +558,7 @@ __device__ __forceinline__ void preload_history(const DevGroup& G, int row, Hist
     const int W = G.hist_len;
     const char* hrow = G.history ? hist_row(G, row) : nullptr;
     if (hrow && !G.hist_i64 && (((uintptr_t)hrow & 15) == 0) && W >= 4 * kThreads) {
-        const int4 v = gp((const int4*)hrow)[threadIdx.x];
+        const int4 v = ld_i4((const int4*)hrow + threadIdx.x);
         P.h[0] = v.x;
         P.h[1] = v.y;
         P.h[2] = v.z;
@@ -706,20 +720,22 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     const int lo = slice * G.slice_len, hi = min(G.vocab, lo + G.slice_len);
     const Geo<ES> geo = slice_geo<ES>(G, row, lo);
     const int w = wave_id(), l = lane_id(), tid = threadIdx.x;
-    // every input load first (the tile, its bitmask words, the row's history); the row's parameters after
-    uint4 t[RMAX];
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r)
-        t[r] = r < RR ? load_chunk<ES>(geo, (w * RR + r) * 64 + l, hi) : make_uint4(0u, 0u, 0u, 0u);
+    // the loads in the order their values are needed (loads return in order): the row's parameters, the history
+    // head and the bitmask words (the LDS set-up runs on them while the tile is in flight), then the tile
+    const RowIn rin = load_row_in(G, row);
+    HistPre hp;
+    preload_history(G, row, hp);
     const int tile_len = kThreads * E * RR;
     const int jb = (geo.first >> 5) << 5;
     const int nkw = min(kKeepWords, (geo.first + tile_len - jb + 31) / 32 + 1);
     uint32_t mw[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) mw[u] = mask_word(G, row, jb, tid + u * kThreads, nkw);
-    HistPre hp;
-    preload_history(G, row, hp);
-    const Row R = make_row(G, gi, row, slice);
+    uint4 t[RMAX];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r)
+        t[r] = r < RR ? load_chunk<ES>(geo, (w * RR + r) * 64 + l, hi) : make_uint4(0u, 0u, 0u, 0u);
+    const Row R = make_row(G, gi, row, slice, rin);
     Rout = R;
     if (R.mode == kSkip) {
         if (slice == 0 && tid == 0 && G.tokens) gp(G.tokens)[row] = kPad;
@@ -1088,26 +1104,20 @@ __device__ __forceinline__ int slice_first(const DevGroup& G, int row, int lo) {
     return lo - (int)((lo_addr & 15) / G.es);
 }
 
-enum : int { kSrcCands = 0, kSrcRow = 1, kSrcHistSlice = 2 };
+enum : int { kSrcCands = 0, kSrcRow = 1 };
 enum : int { kJobStats = 0, kJobHist, kJobSums, kJobSurvMax, kJobSurvSum, kJobOutZ, kJobOut, kJobPick };
 enum : int { kSelCount = 0, kSelCut, kSelDraw };
 
 struct Visit {
     int src, n;       // kSrcCands: n candidates in L.a.c (weighted: the id field holds a multiplicity)
     bool weighted;
-    // kSrcHistSlice: elements [lo, hi) of the row weigh lut[key] (lumps: their own mass when lump_surv), special
-    // positions (L.keep bits from lo rounded down to 32) are skipped, and the nsp specials at spl weigh their own
-    const unsigned long long* lut;
-    const unsigned long long* spl;
-    int nsp;
-    bool lump_surv;
     int lo, hi;       // kSrcRow: elements [lo, hi)
     int job, sel;
     uint32_t lo_k, hi_k;
     int sh;           // kJobHist: keys in [lo_k, hi_k], bins of 2^sh keys
     float kth, thr, m, md;
-    float* prow;
-    float* qrow;
+    gptr<float> prow;
+    gptr<float> qrow;
     float inv;
     // per-thread results
     float f0, f1;
@@ -1180,42 +1190,6 @@ __device__ __forceinline__ void visit(Visit& V, const DevGroup& G, const Row& R,
             const uint32_t id = L.a.c.id[i];
             const uint32_t v = id & ~kSelOnlyBit;
             consume(V, L, L.a.c.q[i], (int)v, !(id & kSelOnlyBit), V.weighted ? (unsigned long long)v : 1ull);
-        }
-        return;
-    }
-    if (V.src == kSrcHistSlice) {  // the draw's histogram rounds over one slice (keys are token ids)
-        const int lo = max(V.lo, (int)V.lo_k), hi = min(V.hi, (int)V.hi_k + 1);
-        const Geo<2> g = slice_geo<2>(G, R.row, lo);
-        const uint32_t* mrow = G.allowed ? gp(G.allowed) + (int64_t)R.row * G.allowed_stride : nullptr;
-        const int jb = (V.lo >> 5) << 5;
-        const int nch = hi > lo ? (hi - g.first + 7) / 8 : 0;
-        for (int c = threadIdx.x; c < nch; c += kThreads) {
-            const uint4 v = load_chunk<2>(g, c, hi);
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-            const int j0 = g.first + 8 * c;
-#pragma unroll
-            for (int h = 0; h < 8; ++h) {
-                const int j = j0 + h;
-                const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
-                if (j < lo || j >= hi || b == 0xff80u) continue;
-                if (mrow && !((mrow[j >> 5] >> (j & 31)) & 1u)) continue;
-                if ((L.keep[(j - jb) >> 5] >> ((j - jb) & 31)) & 1u) continue;  // a special
-                if (R.eos_rule != kEosNormal && j == G.eos) continue;
-                const int k = bf_key(b);
-                unsigned long long w = V.lut[k];
-                if (V.lump_surv && (k == kKeyZero - 1 || k == kKeyZero + 1))
-                    w = efx(to_q<2>(R, __uint_as_float(b << 16)), V.md);
-                if (w) atomicAdd(&L.h.w[((uint32_t)j - V.lo_k) >> V.sh], w);
-            }
-        }
-        for (int i = threadIdx.x; i < V.nsp; i += kThreads) {
-            const unsigned long long e = pub_ld(V.spl + i);
-            const uint32_t id = (uint32_t)(e >> 32);
-            const float q = __uint_as_float((uint32_t)e);
-            const uint32_t j = id & ~kSelOnlyBit;
-            if ((id & kSelOnlyBit) || !(q >= V.thr) || j < V.lo_k || j > V.hi_k) continue;
-            const unsigned long long w = efx(q, V.md);
-            if (w) atomicAdd(&L.h.w[(j - V.lo_k) >> V.sh], w);
         }
         return;
     }
@@ -2450,95 +2424,226 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     out.mdraw = -INFINITY;
     out.token = R.V - 1;
     if (!(m > -INFINITY)) return true;
-    // every slice's counts, merged
+    // every slice's counts, merged (the loads of four slices issued together)
     uint32_t* cnt = (uint32_t*)L.h.w;
-    for (int i = tid; i < kHistWords; i += kThreads) {
+    for (int i0 = 0; i0 < kHistWords; i0 += kThreads) {
+        const int i = i0 + tid;
         uint32_t a = 0u, b = 0u;
-        for (int s = 0; s < S; ++s) {
-            const uint32_t v = pub_ld((const uint32_t*)(rec_base(G, R.row, s) + kRecHistOff) + i);
-            a += v & 0xffffu;
-            b += v >> 16;
+        for (int s0 = 0; s0 < S; s0 += 4) {
+            uint32_t v[4];
+#pragma unroll
+            for (int u4 = 0; u4 < 4; ++u4)
+                v[u4] = (i < kHistWords && s0 + u4 < S)
+                            ? pub_ld((const uint32_t*)(rec_base(G, R.row, s0 + u4) + kRecHistOff) + i)
+                            : 0u;
+#pragma unroll
+            for (int u4 = 0; u4 < 4; ++u4) {
+                a += v[u4] & 0xffffu;
+                b += v[u4] >> 16;
+            }
         }
-        cnt[2 * i] = a;
-        cnt[2 * i + 1] = b;
+        if (i < kHistWords) {
+            cnt[2 * i] = a;
+            cnt[2 * i + 1] = b;
+        }
+    }
+    // the value of every key (a lump takes the value of the exact key below it, so the table is monotone)
+    char* const abase = (char*)&L.a;
+    unsigned long long* mo = (unsigned long long*)abase;  // per key: mass of the specials strictly above its value
+    uint32_t* co = (uint32_t*)(abase + 8 * (kKeys + 1));   // ... and their count
+    float* qt = (float*)(abase + 12 * (kKeys + 1));
+    for (int k = tid; k < kKeys; k += kThreads) {
+        const int ke = key_exact(k) ? k : k - 1;
+        qt[k] = ke >= 1 ? to_q<2>(R, key_bf(ke)) : -INFINITY;
+        mo[k] = 0ull;
+        co[k] = 0u;
     }
     __syncthreads();
     const uint32_t nlump = cnt[kKeyZero - 1] + cnt[kKeyZero + 1];
     if (cnt[kKeys - 1] != 0u) return false;  // values of 256 and above are not resolved here
-    // the weighted list: values present (exact keys), then every special (the censored EOS ranks but is not drawn)
-    float qmax = -INFINITY, nqmin = -INFINITY;
-    for (int k0 = 0; k0 < kKeys; k0 += kThreads) {
-        const int k = k0 + tid;
-        const uint32_t c = (k < kKeys && key_exact(k)) ? cnt[k] : 0u;
-        const int slot = lds_reserve(c != 0u, &L.nspec);
-        if (slot >= 0 && slot < kCapRow) {
-            const float q = to_q<2>(R, key_bf(k));
-            L.a.c.q[slot] = q;
-            L.a.c.id[slot] = c;
-            qmax = fmaxf(qmax, q);
-            nqmin = fmaxf(nqmin, -q);
-        }
-    }
-    __syncthreads();
-    const int n0 = L.nspec;
-    const int n = n0 + ntot;
-    if (n > kCapRow) return false;
-    for (int i = tid; i < ntot; i += kThreads) {
-        int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
+    // every special into its bin: the even bin of the exact key holding its value, or the odd bin strictly between
+    // that key and the next exact one (engine/talker_sampler.py:87-92 ranks values, so equal values share a bin)
+    auto bin_of = [&](float q) -> int {  // 2 k (value of key k) or 2 k + 1 (between); -1 below every key
+        if (!(q >= qt[1])) return -1;
+        int lo = 1, hi = kKeys;  // qt[lo] <= q < qt[hi]
         while (hi - lo > 1) {
             const int mid = (lo + hi) >> 1;
-            if (L.segoff[mid] <= i)
+            if (qt[mid] <= q)
                 lo = mid;
             else
                 hi = mid;
         }
-        const unsigned long long e =
-            pub_ld((const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) + (i - L.segoff[lo]));
-        const float q = __uint_as_float((uint32_t)e);
-        L.a.c.q[n0 + i] = q;
-        L.a.c.id[n0 + i] = 1u | ((uint32_t)(e >> 32) & kSelOnlyBit);
-        if (q > -INFINITY) {
-            qmax = fmaxf(qmax, q);
-            nqmin = fmaxf(nqmin, -q);
+        const int k = key_exact(lo) ? lo : lo - 1;
+        return qt[k] == q ? 2 * k : 2 * k + 1;
+    };
+    for (int i0 = 0; i0 < ntot; i0 += 4 * kThreads) {
+        unsigned long long e[4];
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const int i = i0 + u4 * kThreads + tid;
+            int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (L.segoff[mid] <= i)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
+            e[u4] = i < ntot ? pub_ld((const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) +
+                                      (i - L.segoff[lo]))
+                             : 0ull;
+        }
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const float q = __uint_as_float((uint32_t)e[u4]);
+            if (i0 + u4 * kThreads + tid >= ntot || !(q > -INFINITY)) continue;
+            const int b = bin_of(q);
+            if (b < 0) {
+                atomicAdd(&co[0], 1u);  // below every key: ranks last, weighs nothing at these magnitudes
+            } else if (b & 1) {
+                atomicAdd(&mo[b >> 1], efx(q, m));
+                atomicAdd(&co[b >> 1], 1u);
+            } else {
+                atomicAdd(&cnt[b >> 1], 1u);
+            }
         }
     }
     unsigned long long tiny0 = 0ull;
     for (int s = 0; s < S; ++s) tiny0 += L.slice_u[s];
-    const float4 ext = block_max4(make_float4(qmax, nqmin, -INFINITY, -INFINITY), L.red);
-    const uint32_t k0key = ord_key(0.0f);
-    uint32_t klo = n ? ord_key(-ext.y) : k0key, khi = n ? ord_key(ext.x) : k0key;
-    if (nlump) {
-        klo = min(klo, k0key);
-        khi = max(khi, k0key);
-    }
-    // the cut (engine/talker_sampler.py:87-92 semantics through the fixed-point masses of select_draw)
-    Visit V;
-    V.src = kSrcCands;
-    V.n = n;
-    V.weighted = true;
-    V.lo = V.hi = 0;
-    V.kth = V.thr = V.md = -INFINITY;
-    V.m = m;
-    const float q_tlo = to_q<2>(R, -0.0078125f), q_thi = to_q<2>(R, 0.0078125f);
     const unsigned long long lump_m = nlump ? (unsigned long long)((double)tiny0 * exp(-(double)m)) : 0ull;
+    __syncthreads();
+    // even-bin mass and count of key k (the tiny lumps' mass sits with the positive lump)
+    auto even_mass = [&](int k) -> unsigned long long {
+        if (key_exact(k)) return cnt[k] ? (unsigned long long)cnt[k] * efx(qt[k], m) : 0ull;
+        return k == kKeyZero + 1 ? lump_m : 0ull;
+    };
+    // keys whose bins hold a lump, or the specials beside one (both tiny lumps' mass sits with the positive one):
+    // their order is not resolved here
+    auto near_lump = [&](int k) { return k == 0 || (nlump && k >= kKeyZero - 2 && k <= kKeyZero + 1); };
+    // one descending pass over the keys: thread t holds keys kKeys - 1 - 4 t .. - 3; the first bin (odd bin of k,
+    // then its even bin) at which the cumulative weight reaches T; false when the total is below T
+    auto scan_cut = [&](unsigned long long T, bool by_mass, int& key_out, bool& odd_out,
+                        unsigned long long& before_out) -> bool {
+        unsigned long long wsum = 0ull;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int k = kKeys - 1 - (4 * tid + d);
+            if (k >= 0) wsum += by_mass ? mo[k] + even_mass(k) : (unsigned long long)co[k] + cnt[k];
+        }
+        unsigned long long tot;
+        const unsigned long long ex = block_excl_scan(wsum, tot, L.red.u);
+        if (tid == 0) L.token = -1;
+        __syncthreads();
+        if (ex < T && T <= ex + wsum) {
+            unsigned long long c = ex;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const int k = kKeys - 1 - (4 * tid + d);
+                if (k < 0) break;
+                const unsigned long long wo = by_mass ? mo[k] : co[k];
+                const unsigned long long we = by_mass ? even_mass(k) : cnt[k];
+                if (c + wo >= T) {
+                    L.token = 2 * k + 1;
+                    L.uscratch[1] = c;
+                    break;
+                }
+                c += wo;
+                if (c + we >= T) {
+                    L.token = 2 * k;
+                    L.uscratch[1] = c;
+                    break;
+                }
+                c += we;
+            }
+        }
+        __syncthreads();
+        const int b = L.token;
+        before_out = L.uscratch[1];
+        __syncthreads();
+        if (b < 0) return false;
+        key_out = b >> 1;
+        odd_out = (b & 1) != 0;
+        return true;
+    };
+    // the value at which the cumulative weight reaches T inside odd bin k: its specials sorted by value
+    // (descending), walked from `before`; NaN when it cannot be resolved here
+    auto resolve_odd = [&](int k, unsigned long long T, unsigned long long before, bool by_mass) -> float {
+        float* rq = (float*)(abase + 16 * (kKeys + 1));
+        unsigned long long* rm = (unsigned long long*)(abase + 16 * (kKeys + 1) + 4 * 256);
+        if (tid == 0) L.scnt = 0;
+        __syncthreads();
+        for (int i0 = 0; i0 < ntot; i0 += kThreads) {
+            const int i = i0 + tid;
+            float q = -INFINITY;
+            if (i < ntot) {
+                int lo = 0, hi = S;
+                while (hi - lo > 1) {
+                    const int mid = (lo + hi) >> 1;
+                    if (L.segoff[mid] <= i)
+                        lo = mid;
+                    else
+                        hi = mid;
+                }
+                q = __uint_as_float((uint32_t)pub_ld(
+                    (const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) + (i - L.segoff[lo])));
+            }
+            const bool in = q > -INFINITY && bin_of(q) == 2 * k + 1;
+            const int slot = lds_reserve(in, &L.scnt);
+            if (in && slot < 256) {
+                rq[slot] = q;
+                rm[slot] = by_mass ? efx(q, m) : 1ull;
+            }
+        }
+        __syncthreads();
+        const int n = L.scnt;
+        if (n > 256) return __uint_as_float(0x7fc00000u);
+        if (wave_id() == 0) {
+            unsigned long long v[4];
+#pragma unroll
+            for (int p4 = 0; p4 < 4; ++p4) {
+                const int i = p4 * 64 + lane_id();
+                v[p4] = i < n ? (((unsigned long long)(~ord_key(rq[i]))) << 32) | (unsigned long long)i : ~0ull;
+            }
+            wave_bitonic<4>(v);
+            unsigned long long c = before;
+            int hit = -1;
+#pragma unroll
+            for (int p4 = 0; p4 < 4; ++p4) {
+                const int i = (int)(v[p4] & 0xffffffffull);
+                const unsigned long long wgt = v[p4] != ~0ull ? rm[i] : 0ull;
+                const unsigned long long incl = wave_incl_scan(wgt) + c;
+                const uint64_t h = ballot(v[p4] != ~0ull && incl >= T);
+                if (hit < 0 && h) hit = (int)__builtin_amdgcn_readlane((int)(v[p4] & 0xffffffffull), __ffsll((long long)h) - 1);
+                c = __builtin_amdgcn_readlane((uint32_t)incl, 63) | ((unsigned long long)__builtin_amdgcn_readlane((uint32_t)(incl >> 32), 63) << 32);
+            }
+            if (lane_id() == 0) L.fscratch[2] = hit >= 0 ? rq[hit] : __uint_as_float(0x7fc00000u);
+        }
+        __syncthreads();
+        const float r = L.fscratch[2];
+        __syncthreads();
+        return r;
+    };
+    // the top-p cut (engine/talker_sampler.py:87-92 through fixed-point masses) and the min_keep floor
     const double pt = ceil((double)R.top_p * zn);
     const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
-    uint32_t ckey = 0u;
-    unsigned long long bf;
-    if (!range_find(V, kSelCut, true, T, klo, khi, k0key, lump_m, G, R, L, ckey, bf)) return false;
-    const float thr_p = key_float(ckey);
-    if (nlump && thr_p > q_tlo && thr_p < q_thi) return false;
+    int ck;
+    bool codd;
+    unsigned long long cbef;
+    if (!scan_cut(T, true, ck, codd, cbef)) return false;
+    if (near_lump(ck)) return false;
+    const float thr_p = codd ? resolve_odd(ck, T, cbef, true) : qt[ck];
+    if (!(thr_p == thr_p)) return false;
     float vmk = m;
     if (R.min_keep_eff >= 2) {
-        uint32_t mk = 0u;
-        if (range_find(V, kSelCount, true, (unsigned long long)R.min_keep_eff, klo, khi, k0key, nlump, G, R, L, mk,
-                       bf)) {
-            vmk = key_float(mk);
-            if (nlump && vmk > q_tlo && vmk < q_thi) return false;
+        if (scan_cut((unsigned long long)R.min_keep_eff, false, ck, codd, cbef)) {
+            if (near_lump(ck)) return false;
+            vmk = codd ? resolve_odd(ck, (unsigned long long)R.min_keep_eff, cbef, false) : qt[ck];
+            if (!(vmk == vmk)) return false;
         } else {
             vmk = -INFINITY;
         }
     }
+    const float q_tlo = to_q<2>(R, -0.0078125f);
     const float thr = fminf(thr_p, vmk);
     const float md = mdraw >= thr ? mdraw : -INFINITY;
     out.thr = thr;
@@ -2555,25 +2660,67 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         lut[k] = e;
     }
     const bool lump_surv = nlump && thr <= q_tlo;
+    if (tid < S) L.sbfx[tid] = lump_surv ? (unsigned long long)((double)L.slice_u[tid] * exp(-(double)md)) : 0ull;
     __syncthreads();
-    for (int s = w; s < S; s += kWaves) {
-        const char* rb = rec_base(G, R.row, s);
-        const uint32_t* hg = (const uint32_t*)(rb + kRecHistOff);
-        unsigned long long acc = 0ull;
-        for (int i = l; i < kHistWords; i += 64) {
-            const uint32_t v = pub_ld(hg + i);
-            acc += (unsigned long long)(v & 0xffffu) * lut[2 * i] + (unsigned long long)(v >> 16) * lut[2 * i + 1];
+    // the counts: thread t weighs words t and t + kThreads of every slice's counts, the loads of four slices
+    // issued together; one sum per wave and slice
+    for (int s0 = 0; s0 < S; s0 += 4) {
+        uint32_t v[4][2];
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const uint32_t* hg = (const uint32_t*)(rec_base(G, R.row, min(s0 + u4, S - 1)) + kRecHistOff);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int i = tid + h * kThreads;
+                v[u4][h] = (s0 + u4 < S && i < kHistWords) ? pub_ld(hg + i) : 0u;
+            }
         }
-        const unsigned long long* sg = (const unsigned long long*)(rb + kRecSpecOff);
-        const int ns = L.segoff[s + 1] - L.segoff[s];
-        for (int i = l; i < ns; i += 64) {
-            const unsigned long long e = pub_ld(sg + i);
-            const float q = __uint_as_float((uint32_t)e);
-            if (!((uint32_t)(e >> 32) & kSelOnlyBit) && q >= thr) acc += efx(q, md);
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            unsigned long long acc = 0ull;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int i = min(tid + h * kThreads, kHistWords - 1);
+                acc += (unsigned long long)(v[u4][h] & 0xffffu) * lut[2 * i] +
+                       (unsigned long long)(v[u4][h] >> 16) * lut[2 * i + 1];
+            }
+            acc = wave_sum(acc);
+            if (l == 0 && acc) atomicAdd(&L.sbfx[s0 + u4], acc);
         }
-        acc = wave_reduce(acc, [](unsigned long long a, unsigned long long b) { return a + b; });
-        if (lump_surv) acc += (unsigned long long)((double)L.slice_u[s] * exp(-(double)md));
-        if (l == 0) L.sbfx[s] = acc;
+    }
+    // the specials, flattened over the slices (four loads per thread issued together); per wave, one sum for
+    // each slice its entries span
+    for (int i0 = 0; i0 < ntot; i0 += 4 * kThreads) {
+        unsigned long long e[4];
+        int sl[4];
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const int i = i0 + u4 * kThreads + tid;
+            int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (L.segoff[mid] <= i)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
+            sl[u4] = i < ntot ? lo : -1;
+            e[u4] = i < ntot ? pub_ld((const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) +
+                                      (i - L.segoff[lo]))
+                             : 0ull;
+        }
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const float q = __uint_as_float((uint32_t)e[u4]);
+            const unsigned long long m2 =
+                (sl[u4] >= 0 && !((uint32_t)(e[u4] >> 32) & kSelOnlyBit) && q >= thr) ? efx(q, md) : 0ull;
+            const int smin = wave_reduce(sl[u4] >= 0 ? sl[u4] : S, [](int a, int b) { return min(a, b); });
+            const int smax = wave_reduce(sl[u4], [](int a, int b) { return max(a, b); });
+            for (int sx = smin; sx <= smax; ++sx) {
+                const unsigned long long a = wave_sum(sl[u4] == sx ? m2 : 0ull);
+                if (l == 0 && a) atomicAdd(&L.sbfx[sx], a);
+            }
+        }
     }
     __syncthreads();
     if (tid == 0) {
@@ -2601,33 +2748,116 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     const int ss = L.is_last;
     const unsigned long long rem = L.uscratch[0];
     if (ss < 0) return true;
-    // the draw inside slice ss: its specials as L.keep bits (skipped in the stream, weighed from their list)
+    // the draw inside slice ss in one pass over it: thread t owns chunks [t nc, (t + 1) nc) (8 elements each, from
+    // the slice's 16-byte aligned start) and sums their survivor masses (the specials from their list, added to
+    // their owner); one scan finds the owner of the target, whose wave walks its elements in token order
     const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
-    const int jb = (slo >> 5) << 5;
-    const int nkw = (shi - jb + 31) / 32;
-    for (int k = tid; k < nkw; k += kThreads) L.keep[k] = 0u;
-    __syncthreads();
+    const Geo<2> g = slice_geo<2>(G, R.row, slo);
+    const int nch = (shi - g.first + 7) / 8;
+    const int nc = (nch + kThreads - 1) / kThreads;  // <= kRounds
+    const int jb = (g.first >> 5) << 5;
+    const int nkw = min(kKeepWords, (shi - jb + 31) / 32);
+    uint32_t mwv[2];
+#pragma unroll
+    for (int u2 = 0; u2 < 2; ++u2) mwv[u2] = mask_word(G, R.row, jb, tid + u2 * kThreads, nkw);
+    uint4 cv[kRounds];
+#pragma unroll
+    for (int c = 0; c < kRounds; ++c)
+        cv[c] = c < nc ? load_chunk<2>(g, tid * nc + c, shi) : make_uint4(0u, 0u, 0u, 0u);
+    unsigned long long* tsum = (unsigned long long*)L.a.c.id;  // per thread
+    uint32_t* spid = (uint32_t*)(tsum + kThreads);            // the slice's specials: position and mass
+    unsigned long long* spm = (unsigned long long*)(spid + kSpecCap);
     const unsigned long long* spl = (const unsigned long long*)(rec_base(G, R.row, ss) + kRecSpecOff);
-    const int nsp = L.segoff[ss + 1] - L.segoff[ss];
-    for (int i = tid; i < nsp; i += kThreads) {
-        const int j = (int)((uint32_t)(pub_ld(spl + i) >> 32) & ~kSelOnlyBit);
-        atomicOr(&L.keep[(j - jb) >> 5], 1u << ((j - jb) & 31));
+    const int nsp = min(L.segoff[ss + 1] - L.segoff[ss], kSpecCap);
+    unsigned long long se[2];
+#pragma unroll
+    for (int u2 = 0; u2 < 2; ++u2) se[u2] = tid + u2 * kThreads < nsp ? pub_ld(spl + tid + u2 * kThreads) : 0ull;
+#pragma unroll
+    for (int u2 = 0; u2 < 2; ++u2) {
+        const int k = tid + u2 * kThreads;
+        if (k < kKeepWords) L.keep[k] = k < nkw ? mwv[u2] & range_bits(jb + 32 * k, slo, shi) : 0u;
+    }
+    tsum[tid] = 0ull;
+    __syncthreads();
+    const int eos = G.eos;
+    if (tid == 0 && R.eos_rule != kEosNormal && eos >= slo && eos < shi) clear_keep_bit(L, g.first, eos);
+    const int own_len = 8 * nc;
+#pragma unroll
+    for (int u2 = 0; u2 < 2; ++u2) {
+        const int i = tid + u2 * kThreads;
+        if (i < nsp) {
+            const unsigned long long e = se[u2];
+            const int j = (int)((uint32_t)(e >> 32) & ~kSelOnlyBit);
+            const float q = __uint_as_float((uint32_t)e);
+            const unsigned long long m2 = (!((uint32_t)(e >> 32) & kSelOnlyBit) && q >= thr) ? efx(q, md) : 0ull;
+            clear_keep_bit(L, g.first, j);
+            spid[i] = (uint32_t)(j - g.first);
+            spm[i] = m2;
+            if (m2) atomicAdd(&tsum[(j - g.first) / own_len], m2);
+        }
     }
     __syncthreads();
-    V.src = kSrcHistSlice;
-    V.weighted = false;
-    V.lo = slo;
-    V.hi = shi;
-    V.lut = lut;
-    V.spl = spl;
-    V.nsp = nsp;
-    V.lump_surv = lump_surv;
-    V.thr = thr;
-    V.md = md;
-    uint32_t tok = 0u;
-    if (!range_find(V, kSelDraw, false, rem, (uint32_t)slo, (uint32_t)(shi - 1), 0u, 0ull, G, R, L, tok, bf))
-        return false;
-    out.token = (int64_t)tok;
+    // survivor mass of the element at bf16 bits b whose keep bit is set
+    auto elem_mass = [&](uint32_t b) -> unsigned long long {
+        const int k = bf_key(b);
+        if (lump_surv && (k == kKeyZero - 1 || k == kKeyZero + 1)) return efx(to_q<2>(R, __uint_as_float(b << 16)), md);
+        return lut[k];
+    };
+    unsigned long long acc = 0ull;
+#pragma unroll
+    for (int c = 0; c < kRounds; ++c) {
+        if (c >= nc) continue;
+        const uint32_t kb = chunk_keep<2>(L, g.first, tid * nc + c);
+        const uint32_t wv[4] = {cv[c].x, cv[c].y, cv[c].z, cv[c].w};
+#pragma unroll
+        for (int h = 0; h < 8; ++h)
+            if ((kb >> h) & 1u) acc += elem_mass((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu);
+    }
+    const unsigned long long mine = tsum[tid] + acc;
+    unsigned long long tot;
+    const unsigned long long ex = block_excl_scan(mine, tot, L.red.u);
+    if (tid == 0) L.token = -1;
+    __syncthreads();
+    if (mine && ex < rem && rem <= ex + mine) {
+        L.token = tid;
+        L.uscratch[1] = rem - ex;
+    }
+    __syncthreads();
+    const int own = L.token;
+    if (own < 0) return false;  // the slice holds less than its share (the lumps' summed masses round differently)
+    // the owner's chunks and keep bits to LDS; its specials' masses by position
+    uint4* ochunk = (uint4*)L.gh;
+    unsigned long long* om = L.sbfx;  // own_len <= 8 kRounds entries
+    if (tid == own) {
+#pragma unroll
+        for (int c = 0; c < kRounds; ++c)
+            if (c < nc) ochunk[c] = cv[c];
+    }
+    if (tid < own_len) om[tid] = 0ull;
+    __syncthreads();
+    for (int i = tid; i < nsp; i += kThreads) {
+        const int pos = (int)spid[i] - own * own_len;
+        if (pos >= 0 && pos < own_len) om[pos] = spm[i];
+    }
+    __syncthreads();
+    if (wave_id() == 0) {
+        const int i = lane_id();
+        unsigned long long wm = 0ull;
+        if (i < own_len) {
+            const int c = i >> 3, h = i & 7;
+            const uint4 v = ochunk[min(c, kRounds - 1)];
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t kb = chunk_keep<2>(L, g.first, own * nc + c);
+            wm = ((kb >> h) & 1u) ? elem_mass((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu) : om[i];
+        }
+        const unsigned long long incl = wave_incl_scan(wm);
+        const uint64_t hit = ballot(wm && incl >= L.uscratch[1]);
+        if (lane_id() == 0)
+            L.uscratch[0] = hit ? (unsigned long long)(g.first + own * own_len + __ffsll((long long)hit) - 1) : ~0ull;
+    }
+    __syncthreads();
+    if (L.uscratch[0] == ~0ull) return false;
+    out.token = (int64_t)L.uscratch[0];
     return true;
 }
 
@@ -2713,8 +2943,8 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
 
 // Processed logits and probabilities of the whole row (parity outputs), streamed.
 __device__ __forceinline__ void write_outputs(const DevGroup& G, const Row& R, Lds& L, const Outcome& o, bool forced) {
-    float* prow = G.processed ? gp(G.processed) + (int64_t)R.row * G.processed_stride : nullptr;
-    float* qrow = G.probs ? gp(G.probs) + (int64_t)R.row * G.probs_stride : nullptr;
+    const gptr<float> prow = G.processed ? gp(G.processed) + (int64_t)R.row * G.processed_stride : nullptr;
+    const gptr<float> qrow = G.probs ? gp(G.probs) + (int64_t)R.row * G.probs_stride : nullptr;
     if (forced) {
         for (int j = threadIdx.x; j < R.V; j += kThreads) {
             const bool e = j == G.eos;
