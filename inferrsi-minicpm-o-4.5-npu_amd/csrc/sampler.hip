@@ -132,6 +132,7 @@ struct SliceRec {
     int32_t hist;    // 1: the nucleus histogram and the specials list are published
     int32_t nspec;   // specials published
     double z;        // sum of exp(q - mref) (whole-vocabulary normaliser, unfiltered rows)
+    double zc;       // the part of z over the published candidates (top-p rows without top-k)
     int32_t ncand[kSegs];
     int32_t pad0;
     unsigned long long tinyfx;  // sum of exp(q) in fixed point over the tiny-magnitude lumps of the histogram
@@ -147,6 +148,9 @@ constexpr int kKeyZero = 1922;
 constexpr uint32_t kBfLo = 0x3C00u;  // 2^-7
 constexpr uint32_t kBfHi = 0x4380u;  // 2^8
 constexpr int kHistWords = (kKeys + 1) / 2;  // published as u16 pairs
+constexpr int kHistReps = 4;                 // copies of a slice's counts while it builds them
+constexpr int kHistStride = 3848;            // words per copy: kKeys + 1 rounded up to 8 (copies 8 banks apart)
+static_assert(kHistReps * kHistStride <= kCntWords && kHistStride >= 2 * kHistWords, "histogram copies");
 constexpr int64_t kRecHistOff = kRecCandOff + 8 * (kWaves * kCapWave + kCapSpecSeg);
 constexpr int64_t kRecSpecOff = kRecHistOff + 4 * ((kHistWords + 63) / 64 * 64);
 constexpr int64_t kRecBytes = kRecSpecOff + 8 * kSpecCap;
@@ -961,14 +965,16 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     unsigned long long* segs = (unsigned long long*)((char*)rec + kRecCandOff);
     unsigned long long* myseg = segs + (int64_t)w * kCapWave;
     int cnt = 0, flags = 0;
-    double zacc = 0.0;
+    double zacc = 0.0, cacc = 0.0;
     const float mref = mq;
     // bf16 top-p rows without top-k also publish the count of every value (the nucleus histogram) and their
     // specials, which settle a nucleus wider than the candidates
     const bool hist = ES == 2 && R.mode == kNucleus && R.T >= 0.015625f;
     if (hist) {
-        uint32_t* hk = (uint32_t*)L.h.w;
-        for (int i = tid; i < 2 * kBins; i += kThreads) hk[i] = 0u;
+        // kHistReps copies of the counts (the history counts are no longer needed): lane l adds to copy l % kHistReps,
+        // so lanes of a wave that hold one value spread their LDS atomics over several addresses and banks
+        uint4* hk4 = (uint4*)L.a.cnt;
+        for (int i = tid; i < kHistReps * kHistStride / 4; i += kThreads) hk4[i] = make_uint4(0u, 0u, 0u, 0u);
         if (tid == 0) L.tinyfx = 0ull;
     }
 #pragma unroll
@@ -984,7 +990,9 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             bits |= (x >= gate && x > -INFINITY) ? (1u << e) : 0u;
             if (R.needz) {
                 const float q = to_q<ES>(R, x);
-                if (q > -INFINITY) zacc += (double)exp_acc(q - mref);
+                const double ex = q > -INFINITY ? (double)exp_acc(q - mref) : 0.0;
+                zacc += ex;
+                if (x >= gate) cacc += ex;
             }
         }
         const int nb = __popc(bits);
@@ -1014,8 +1022,12 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         const bool in = i < ns;
         const float q = in ? L.spec[i].q : -INFINITY;
         const uint32_t id = in ? ((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) : 0u;
-        if (R.needz && q > -INFINITY) zacc += (double)exp_acc(q - mref);
         const bool pred = q >= gate_q && q > -INFINITY;
+        if (R.needz && q > -INFINITY) {
+            const double ex = (double)exp_acc(q - mref);
+            zacc += ex;
+            if (pred) cacc += ex;
+        }
         const int slot = lds_reserve(pred, &L.scnt);
         if (pred) {
             if (slot < kCapSpecSeg)
@@ -1024,18 +1036,22 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 flags |= kRecOverflow;
         }
     }
-    if (R.needz) zacc = wave_reduce(zacc, [](double a, double b) { return a + b; });
+    if (R.needz) {
+        zacc = wave_reduce(zacc, [](double a, double b) { return a + b; });
+        cacc = wave_reduce(cacc, [](double a, double b) { return a + b; });
+    }
     flags = wave_reduce(flags, [](int a, int b) { return a | b; });
     __syncthreads();
     if (l == 0) {
         L.segoff[w] = cnt;
         L.red.d[w] = zacc;
+        L.sb[w] = cacc;
         if (flags) atomicOr(&L.flags, flags);
     }
     if constexpr (ES == 2) {
         if (hist) {
             // counts by value key; the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
-            uint32_t* hk = (uint32_t*)L.h.w;
+            uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
             unsigned long long tf = 0ull;
 #pragma unroll
             for (int r = 0; r < RMAX; ++r) {
@@ -1058,18 +1074,30 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     }
     __syncthreads();
     if (hist) {
-        const uint32_t* hk = (const uint32_t*)L.h.w;
+        const uint32_t* hk = L.a.cnt;
         uint32_t* hg = (uint32_t*)((char*)rec + kRecHistOff);
-        for (int i = tid; i < kHistWords; i += kThreads) hg[i] = hk[2 * i] | (hk[2 * i + 1] << 16);
+        for (int i = tid; i < kHistWords; i += kThreads) {
+            uint32_t a = 0u, b = 0u;
+#pragma unroll
+            for (int c = 0; c < kHistReps; ++c) {
+                a += hk[c * kHistStride + 2 * i];
+                b += hk[c * kHistStride + 2 * i + 1];
+            }
+            hg[i] = a | (b << 16);
+        }
         unsigned long long* sg = (unsigned long long*)((char*)rec + kRecSpecOff);
         for (int i = tid; i < ns; i += kThreads)
             sg[i] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
                     __float_as_uint(L.spec[i].q);
     }
     if (tid == 0) {
-        double z = 0.0;
+        double z = 0.0, zc = 0.0;
 #pragma unroll
-        for (int i = 0; i < kWaves; ++i) z += L.red.d[i];
+        for (int i = 0; i < kWaves; ++i) {
+            z += L.red.d[i];
+            zc += L.sb[i];
+        }
+        rec->zc = zc;
         rec->ncand[kWaves] = min(L.scnt, kCapSpecSeg);
         rec->mq = mq;
         rec->mqd = mqd;
@@ -2254,7 +2282,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         // records (lane s: slice s) and segment counts (lane l: segments [l * per, (l + 1) * per))
         const float u = row_uniform(G, R);
         float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
-        double zz = 0.0;
+        double zz = 0.0, zcc = 0.0;
         int over = 0, notinf = 0;
         if (l < S) {
             const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
@@ -2262,6 +2290,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
             gt = pub_ld(&rec->gate);
             mr = pub_ld(&rec->mref);
             zz = pub_ld(&rec->z);
+            zcc = pub_ld(&rec->zc);
             const int fl = pub_ld(&rec->flags);
             over = (fl & kRecOverflow) ? 1 : 0;
             notinf = (fl & kRecGateInf) ? 0 : 1;
@@ -2279,9 +2308,15 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         const float gate = wave_reduce(gt, [](float a, float b) { return fmaxf(a, b); });
         const int anyover = wave_reduce(over, [](int a, int b) { return max(a, b); });
         const int anyfin = wave_reduce(notinf, [](int a, int b) { return max(a, b); });
-        double zs = 0.0;
-        if (R.needz)
-            zs = wave_sum((mr > -INFINITY && m_sel > -INFINITY) ? zz * exp((double)mr - (double)m_sel) : 0.0);
+        double zs = 0.0, zcs = 0.0;
+        if (R.needz) {
+            const double sc = (mr > -INFINITY && m_sel > -INFINITY) ? exp((double)mr - (double)m_sel) : 0.0;
+            zs = wave_sum(zz * sc);
+            zcs = wave_sum(zcc * sc);
+        }
+        // a top-p row without top-k whose candidates weigh clearly less than top_p of the row cannot be cut among
+        // them: straight to the slices' histograms
+        const int short_mass = (R.mode == kNucleus && R.p_active && zcs < (double)R.top_p * zs * (1.0 - 1e-6)) ? 1 : 0;
         const int incl = wave_incl_scan(mine);
         int o = incl - mine;
 #pragma unroll
@@ -2297,7 +2332,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
             L.fscratch[1] = gate;
             L.fscratch[2] = u;
             L.dscratch[0] = zs;
-            L.token = anyover;
+            L.token = anyover | short_mass;
             L.is_last = anyfin;
             L.uscratch[0] = 0xffffffffull;  // min key, max key of the candidates (below)
             L.uscratch[1] = 0ull;
@@ -2307,28 +2342,40 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
     const int n = L.segoff[nseg];
     if (L.token || n > kCapCand) return false;
     const float m_sel = L.fscratch[0];
-    // gather, with each candidate's mass relative to the row max
+    // gather, with each candidate's mass relative to the row max: four loads per thread issued together
     uint32_t kmin = 0xffffffffu, kmax = 0u;
-    for (int i = tid; i < n; i += kThreads) {
-        int lo = 0, hi = nseg;  // segment: segoff[lo] <= i < segoff[lo + 1]
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (L.segoff[mid] <= i)
-                lo = mid;
-            else
-                hi = mid;
+    for (int i0 = 0; i0 < n; i0 += 4 * kThreads) {
+        unsigned long long v[4];
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const int i = i0 + u4 * kThreads + tid;
+            v[u4] = 0ull;
+            if (i0 + u4 * kThreads >= n) continue;  // the whole batch is past the end
+            int lo = 0, hi = nseg;  // segment: segoff[lo] <= i < segoff[lo + 1]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (L.segoff[mid] <= i)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
+            const int s = lo / kSegs, sg = lo % kSegs;
+            const unsigned long long* seg =
+                (const unsigned long long*)(rec_base(G, R.row, s) + kRecCandOff) + (int64_t)sg * kCapWave;
+            if (i < n) v[u4] = pub_ld(seg + (i - L.segoff[lo]));
         }
-        const int s = lo / kSegs, sg = lo % kSegs;
-        const unsigned long long* seg =
-            (const unsigned long long*)(rec_base(G, R.row, s) + kRecCandOff) + (int64_t)sg * kCapWave;
-        const unsigned long long v = pub_ld(seg + (i - L.segoff[lo]));
-        const float q = __uint_as_float((uint32_t)v);
-        L.a.w.q[i] = q;
-        L.a.w.id[i] = (uint32_t)(v >> 32);
-        L.a.w.mass[i] = efx(q, m_sel);
-        const uint32_t k = ord_key(q);
-        kmin = min(kmin, k);
-        kmax = max(kmax, k);
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            const int i = i0 + u4 * kThreads + tid;
+            if (i >= n) continue;
+            const float q = __uint_as_float((uint32_t)v[u4]);
+            L.a.w.q[i] = q;
+            L.a.w.id[i] = (uint32_t)(v[u4] >> 32);
+            L.a.w.mass[i] = efx(q, m_sel);
+            const uint32_t k = ord_key(q);
+            kmin = min(kmin, k);
+            kmax = max(kmax, k);
+        }
     }
     kmin = wave_reduce(kmin, [](uint32_t a, uint32_t b) { return min(a, b); });
     kmax = wave_reduce(kmax, [](uint32_t a, uint32_t b) { return max(a, b); });
@@ -2465,13 +2512,26 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     // that key and the next exact one (engine/talker_sampler.py:87-92 ranks values, so equal values share a bin)
     auto bin_of = [&](float q) -> int {  // 2 k (value of key k) or 2 k + 1 (between); -1 below every key
         if (!(q >= qt[1])) return -1;
-        int lo = 1, hi = kKeys;  // qt[lo] <= q < qt[hi]
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (qt[mid] <= q)
-                lo = mid;
-            else
-                hi = mid;
+        // the largest key whose value is <= q: the bf16 value nearest q T is within a key or two of it (q is x / T
+        // rounded once for the bf16 x of an exact key, and a special lies between two such values)
+        const uint32_t yb = __float_as_uint(q * R.T);
+        int lo = min(max(bf_key((yb + 0x7fffu + ((yb >> 16) & 1u)) >> 16), 1), kKeys - 1);
+        for (int it = 0; it < 4; ++it) {
+            if (qt[lo] > q)
+                --lo;
+            else if (lo + 1 < kKeys && qt[lo + 1] <= q)
+                ++lo;
+        }
+        if (!(qt[lo] <= q && (lo + 1 >= kKeys || q < qt[lo + 1]))) {
+            lo = 1;
+            int hi = kKeys;  // qt[lo] <= q < qt[hi]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (qt[mid] <= q)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
         }
         const int k = key_exact(lo) ? lo : lo - 1;
         return qt[k] == q ? 2 * k : 2 * k + 1;
@@ -2809,9 +2869,18 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         if (c >= nc) continue;
         const uint32_t kb = chunk_keep<2>(L, g.first, tid * nc + c);
         const uint32_t wv[4] = {cv[c].x, cv[c].y, cv[c].z, cv[c].w};
+        if (lump_surv) {
 #pragma unroll
-        for (int h = 0; h < 8; ++h)
-            if ((kb >> h) & 1u) acc += elem_mass((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu);
+            for (int h = 0; h < 8; ++h)
+                if ((kb >> h) & 1u) acc += elem_mass((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu);
+        } else {
+            // every key's mass read before any is added (independent LDS reads in flight together)
+            unsigned long long mv[8];
+#pragma unroll
+            for (int h = 0; h < 8; ++h) mv[h] = lut[bf_key((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu)];
+#pragma unroll
+            for (int h = 0; h < 8; ++h) acc += ((kb >> h) & 1u) ? mv[h] : 0ull;
+        }
     }
     const unsigned long long mine = tsum[tid] + acc;
     unsigned long long tot;
