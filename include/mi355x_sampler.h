@@ -143,6 +143,15 @@ size_t mis_workspace_bytes(const MisGroup* groups, int n_groups);
  * that share a workspace must be ordered on one stream. */
 int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t workspace_bytes, void* stream);
 
+/* mis_sample on a workspace the library owns, for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  The workspace is a device
+ * array of MIS_STATIC_WORKSPACE_BYTES in the library's code object (one copy per GPU, zero at load); this call
+ * allocates nothing and fails with MIS_E_WORKSPACE when mis_workspace_bytes(groups) exceeds it.  Every call on a
+ * GPU shares that GPU's array: calls that overlap on one GPU (different streams, concurrent graph replays) race
+ * and must not be issued; calls ordered on one stream are safe. */
+#define MIS_STATIC_WORKSPACE_BYTES (64u << 20)
+int mis_sample_static(const MisGroup* groups, int n_groups, void* stream);
+
 /* out[i] = U[0,1) of (seeds[i], steps[i], row_ids[i]) under MIS_RNG_COUNTER (row_ids ignored) or
  * MIS_RNG_PHILOX (row_ids NULL = 0): engine/talker_sampler.py:70-76 for the counter hash. */
 int mis_uniform(const int64_t* seeds, const int64_t* steps, const int64_t* row_ids, int64_t n, int32_t rng, float* out,

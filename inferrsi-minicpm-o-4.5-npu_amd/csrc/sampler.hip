@@ -24,6 +24,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstdarg>
+#include <mutex>
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -3178,6 +3179,33 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+// The workspace of mis_sample_static: a file-scope device array, so that callers that cannot allocate (code under
+// graph capture, serving loops) need not.  Every GPU the library runs on holds its own copy, zero when the code
+// object loads, until the process ends; each launch leaves its arrival words zero again, so the next call on that
+// GPU starts clean.  Host code uses the per-device address from hipGetSymbolAddress, never the array's name.
+constexpr size_t kStaticWsBytes = (size_t)MIS_STATIC_WORKSPACE_BYTES;
+__device__ __align__(256) unsigned char scratch[kStaticWsBytes];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up once per device, with that device current).
+int static_workspace(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(-1, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(MIS_E_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return fail(-1, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return 0;
+}
+
 struct Plan {
     int S, R, slice_len;
 };
@@ -3377,6 +3405,18 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(-1, "launch failed: %s", hipGetErrorString(e));
     return 0;
+}
+
+int mis_sample_static(const MisGroup* groups, int n_groups, void* stream) {
+    g_err.clear();
+    const size_t need = mis_workspace_bytes(groups, n_groups);
+    if (need == 0) return mis_sample(groups, n_groups, nullptr, 0, stream);  // reports the argument error
+    if (need > kStaticWsBytes)
+        return fail(MIS_E_WORKSPACE, "these groups need %zu bytes of workspace; the static workspace holds %zu", need,
+                    kStaticWsBytes);
+    void* ws = nullptr;
+    if (int rc = static_workspace(&ws)) return rc;
+    return mis_sample(groups, n_groups, ws, kStaticWsBytes, stream);
 }
 
 int mis_uniform(const int64_t* seeds, const int64_t* steps, const int64_t* row_ids, int64_t n, int32_t rng, float* out,

@@ -22,6 +22,7 @@ MIS_HISTORY_WINDOW, MIS_HISTORY_RING = 0, 1
 MIS_TOPK_ZERO_DISABLES, MIS_TOPP_ONE_DISABLES, MIS_UPDATE_STATE, MIS_FINALIZE_STREAMING = 1, 2, 4, 8
 MIS_E_ARG, MIS_E_WORKSPACE, MIS_E_UNSUPPORTED = 1, 2, 3
 MIS_WS_PATH_OFFSET = 64
+MIS_STATIC_WORKSPACE_BYTES = 64 << 20
 PATHS = ("greedy", "full", "candidates", "histogram", "stream", "forced")  # MIS_PATH_* order
 
 _vp = ctypes.c_void_p
@@ -49,7 +50,8 @@ class MisGroup(ctypes.Structure):
     ]
 
 
-EXPORTS = ("mis_version", "mis_sizeof_group", "mis_last_error", "mis_workspace_bytes", "mis_sample", "mis_uniform")
+EXPORTS = ("mis_version", "mis_sizeof_group", "mis_last_error", "mis_workspace_bytes", "mis_sample", "mis_sample_static",
+           "mis_uniform")
 
 _lock = threading.Lock()
 _handle: ctypes.CDLL | None = None
@@ -71,6 +73,8 @@ def load(path: Path | str = LIB_PATH) -> ctypes.CDLL:
     h.mis_workspace_bytes.argtypes = [ctypes.POINTER(MisGroup), ctypes.c_int]
     h.mis_sample.restype = ctypes.c_int
     h.mis_sample.argtypes = [ctypes.POINTER(MisGroup), ctypes.c_int, _vp, ctypes.c_size_t, _vp]
+    h.mis_sample_static.restype = ctypes.c_int
+    h.mis_sample_static.argtypes = [ctypes.POINTER(MisGroup), ctypes.c_int, _vp]
     h.mis_uniform.restype = ctypes.c_int
     h.mis_uniform.argtypes = [_vp, _vp, _vp, _i64, _i32, _vp, _vp]
     if h.mis_version() != MIS_ABI_VERSION:
@@ -156,6 +160,13 @@ def sample(groups: list[MisGroup], device: torch.device) -> None:
         check(lib().mis_sample(arr, len(groups), None, 0, None))  # reports the argument error
     ws = workspace(device, need)
     check(lib().mis_sample(arr, len(groups), ws.data_ptr(), ws.numel(), stream_handle(device)))
+
+
+def sample_static(groups: list[MisGroup], device: torch.device) -> None:
+    """One launch on the library's own workspace (``mis_sample_static``): allocates nothing, for callers that
+    cannot allocate; launches that overlap on one GPU race."""
+    arr = (MisGroup * len(groups))(*groups)
+    check(lib().mis_sample_static(arr, len(groups), stream_handle(device)))
 
 
 def uniform(seeds: torch.Tensor, steps: torch.Tensor, row_ids: torch.Tensor | None, rng: int) -> torch.Tensor:

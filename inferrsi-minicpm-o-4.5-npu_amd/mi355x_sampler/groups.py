@@ -178,6 +178,17 @@ def launch(groups: list[RowGroup]) -> None:
     _lib.sample([g.struct for g in groups], dev)
 
 
+def launch_static(groups: list[RowGroup]) -> None:
+    """``launch`` on the library's own workspace (no allocation; launches that overlap on one GPU race)."""
+    if not groups:
+        return
+    dev = groups[0].device
+    for g in groups[1:]:
+        if g.device != dev:
+            raise ValueError("all groups of a launch must be on one device")
+    _lib.sample_static([g.struct for g in groups], dev)
+
+
 def sample(logits: torch.Tensor, **kw) -> RowGroup:
     """One group, one launch; returns the group (``.tokens``, ``.processed``, ``.probs``)."""
     g = RowGroup(logits, **kw)
