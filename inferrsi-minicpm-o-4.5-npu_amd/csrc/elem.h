@@ -59,11 +59,16 @@ __host__ __device__ __forceinline__ float philox_uniform(int64_t seed, int64_t s
 
 // ------------------------------------------------------------------ element arithmetic
 
-// x / d rounded once to float, for any float x and a divisor d > 0 given as rd = RN64(1 / d): the double product
-// x * rd is within 2^-52 of x / d, and a quotient of two 24-bit significands is never within 2^-49 (relative) of a
-// float rounding midpoint unless it is exactly representable, so rounding the product to float gives RN(x / d).
+// x / d rounded once to float (IEEE division) for d > 0 given with rd = RN64(1 / d).  In the normal range the double
+// product x * rd is within 2^-52 (relative) of x / d, while a quotient of two 24-bit significands is either a float
+// or at least 2^-49 (relative) away from every float rounding midpoint, so rounding the product to float gives
+// RN(x / d).  Below 2^-126 float midpoints are 2^-150 apart and a quotient can sit exactly on one, where the
+// product may fall on either side: a result under 2^-125 in magnitude is therefore recomputed by IEEE division.
 // Infinities, zeros (with their sign) and NaN pass through as IEEE division has them.
-__device__ __forceinline__ float div_rn(float x, double rd) { return (float)((double)x * rd); }
+__device__ __forceinline__ float div_rn(float x, float d, double rd) {
+    const float q = (float)((double)x * rd);
+    return (fabsf(q) < 0x1p-125f && x != 0.0f) ? x / d : q;
+}
 
 // exp(x) within ~1.3 ulp: 2^(x log2 e) with the product's rounding error (and log2 e's own) folded back in
 // first order, on the hardware exp2.

@@ -316,7 +316,7 @@ __device__ __forceinline__ Row make_row(const DevGroup& G, int gi, int row, int 
 
 __device__ __forceinline__ float penalize(const Row& R, const DevGroup& G, float x, int n) {
     const float a = alpha_of(R.rep, n, G.alpha_lut, G.alpha_lut_len);
-    x = x < 0.f ? x * a : div_rn(x, 1.0 / (double)a);
+    x = x < 0.f ? x * a : div_rn(x, a, 1.0 / (double)a);
     x = x - R.freq * (float)n;
     return x - R.pres;
 }
@@ -327,13 +327,13 @@ __device__ __forceinline__ float elem_q(const Row& R, const DevGroup& G, float x
     if (R.eos_rule == kEosExcluded && j == G.eos) return -INFINITY;
     const bool pn = R.pen && n > 0;
     if (R.hf) {
-        x = div_rn(x, R.rT);
+        x = div_rn(x, R.T, R.rT);
         if (pn) x = penalize(R, G, x, n);
         if (!allowed) x = -INFINITY;
     } else {
         if (pn) x = penalize(R, G, x, n);
         if (!allowed) x = -INFINITY;
-        x = div_rn(x, R.rT);
+        x = div_rn(x, R.T, R.rT);
     }
     return x;
 }
@@ -680,7 +680,7 @@ __device__ __forceinline__ float tile_val_dyn(const uint4& v, int e) {
 
 template <int ES>
 __device__ __forceinline__ float to_q(const Row& R, float x) {
-    return ES == 2 ? div_rn(x, R.rT) : x;
+    return ES == 2 ? div_rn(x, R.T, R.rT) : x;
 }
 
 // Histogram key of a finite bf16 value b (raw bits); -0 is zero.  Keys increase with the value.
@@ -834,7 +834,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         } else {
             float f[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) f[e] = ((kb >> e) & 1u) ? div_rn(f[e], R.rT) : -INFINITY;
+            for (int e = 0; e < 4; ++e) f[e] = ((kb >> e) & 1u) ? div_rn(f[e], R.T, R.rT) : -INFINITY;
             v = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
         }
         t[r] = v;

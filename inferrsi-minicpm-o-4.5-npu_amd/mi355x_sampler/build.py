@@ -54,5 +54,19 @@ def build(verbose: bool = False) -> Path:
     return OUT
 
 
+def build_probe(src: Path, out: Path, verbose: bool = False) -> Path:
+    """A test-only HIP library from one source next to the tests (same flags and headers as the sampler)."""
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{PKG_ROOT / 'csrc'}", "-o", str(tmp), str(src)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out_txt = "\n".join(line for line in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in line)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{out_txt}")
+    if verbose and out_txt.strip():
+        print(out_txt, file=sys.stderr)
+    os.replace(tmp, out)
+    return out
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
