@@ -38,6 +38,26 @@
 namespace mis {
 namespace {
 
+// Phase timestamps (the 100 MHz real-time counter, thread 0 of each workgroup), for profiling the slice and
+// finaliser phases; compiled in with -DMIS_PHASE_STAMPS only.
+#ifdef MIS_PHASE_STAMPS
+constexpr int kStampSlots = 32;
+constexpr int kStampBlocks = 8192;
+__device__ unsigned long long mis_stamps[kStampBlocks * kStampSlots];
+#define MIS_STAMP(i)                                                                                         \
+    do {                                                                                                     \
+        if (threadIdx.x == 0 && blockIdx.x < kStampBlocks)                                                   \
+            mis_stamps[blockIdx.x * kStampSlots + (i)] = __builtin_amdgcn_s_memrealtime();                   \
+    } while (0)
+#define MIS_STAMP_INFO(v)                                                                                    \
+    do {                                                                                                     \
+        if (threadIdx.x == 0 && blockIdx.x < kStampBlocks) mis_stamps[blockIdx.x * kStampSlots + 31] = (v); \
+    } while (0)
+#else
+#define MIS_STAMP(i) ((void)0)
+#define MIS_STAMP_INFO(v) ((void)0)
+#endif
+
 constexpr int kMaxGroups = 4;
 constexpr int kMaxSlices = 64;
 constexpr int kMaxRows = 16384;
@@ -132,8 +152,8 @@ struct SliceRec {
     int32_t flags;   // kRec*
     int32_t hist;    // 1: the nucleus histogram and the specials list are published
     int32_t nspec;   // specials published
-    double z;        // sum of exp(q - mref) (whole-vocabulary normaliser, unfiltered rows)
-    double zc;       // the part of z over the published candidates (top-p rows without top-k)
+    double z;        // sum of exp(q - mref) (whole-vocabulary normaliser)
+    double zc;       // the part of z over the published candidates
     int32_t ncand[kSegs];
     int32_t pad0;
     unsigned long long tinyfx;  // sum of exp(q) in fixed point over the tiny-magnitude lumps of the histogram
@@ -154,7 +174,9 @@ constexpr int kHistStride = 3848;            // words per copy: kKeys + 1 rounde
 static_assert(kHistReps * kHistStride <= kCntWords && kHistStride >= 2 * kHistWords, "histogram copies");
 constexpr int64_t kRecHistOff = kRecCandOff + 8 * (kWaves * kCapWave + kCapSpecSeg);
 constexpr int64_t kRecSpecOff = kRecHistOff + 4 * ((kHistWords + 63) / 64 * 64);
-constexpr int64_t kRecBytes = kRecSpecOff + 8 * kSpecCap;
+constexpr int64_t kRecSpecBinOff = kRecSpecOff + 8 * kSpecCap;  // the specials' histogram bins + 1 (u32)
+constexpr int64_t kRecBytes = kRecSpecBinOff + 4 * kSpecCap;
+constexpr float kHistMinT = 0.015625f;  // the histogram path serves temperatures >= 2^-6 (lumps stay near 0)
 
 struct Special {
     int32_t j;    // token id
@@ -476,6 +498,7 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 
 // Every thread: true in the row's last workgroup to arrive.  Sets L.foreign.
 __device__ __forceinline__ bool arrive(const KernelArgs& A, const Row& R, Lds& L) {
+    MIS_STAMP(5);
     if (R.S == 1) {
         wait_stores();
         __syncthreads();
@@ -498,6 +521,7 @@ __device__ __forceinline__ bool arrive(const KernelArgs& A, const Row& R, Lds& L
         L.foreign = (old & ~(255ull << (8 * x))) != 0ull;
     }
     __syncthreads();
+    MIS_STAMP(6);
     return L.is_last != 0;
 }
 
@@ -711,6 +735,48 @@ __device__ __forceinline__ float key_bf(int k) {
     return __uint_as_float(b << 16);
 }
 
+// The value of key k in the processed domain; a lump takes the value of the exact key below it, so the values
+// never decrease with the key; -inf for key 0.
+__device__ __forceinline__ float key_q(const Row& R, int k) {
+    const int ke = key_exact(k) ? k : k - 1;
+    return ke >= 1 ? to_q<2>(R, key_bf(ke)) : -INFINITY;
+}
+
+// Histogram bin of a processed value q (a special's): 2 k when q is the value of exact key k, 2 k + 1 when it lies
+// strictly between that value and the next key's; -1 below every key.  qt(k) is key_q(R, k) (computed or from a
+// table).  engine/talker_sampler.py:87-92 ranks values, so equal values share a bin.
+template <class QT>
+__device__ __forceinline__ int hist_bin(const Row& R, float q, QT&& qt) {
+    if (!(q >= qt(1))) return -1;
+    // the largest key whose value is <= q: the bf16 value nearest q T is within a key or two of it (q is x / T
+    // rounded once for the bf16 x of an exact key, and a special lies between two such values)
+    const uint32_t yb = __float_as_uint(q * R.T);
+    int lo = min(max(bf_key((yb + 0x7fffu + ((yb >> 16) & 1u)) >> 16), 1), kKeys - 1);
+    for (int it = 0; it < 4; ++it) {
+        if (qt(lo) > q)
+            --lo;
+        else if (lo + 1 < kKeys && qt(lo + 1) <= q)
+            ++lo;
+    }
+    if (!(qt(lo) <= q && (lo + 1 >= kKeys || q < qt(lo + 1)))) {
+        lo = 1;
+        int hi = kKeys;  // qt(lo) <= q < qt(hi)
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (qt(mid) <= q)
+                lo = mid;
+            else
+                hi = mid;
+        }
+    }
+    const int k = key_exact(lo) ? lo : lo - 1;
+    return qt(k) == q ? 2 * k : 2 * k + 1;
+}
+
+// Top-p rows without top-k on bf16 logits are settled from value counts (the histogram path).
+__device__ __forceinline__ bool nucleus_hist(const Row& R, int es) {
+    return es == 2 && R.mode == kNucleus && R.T >= kHistMinT;
+}
 
 enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2 };
 
@@ -742,6 +808,8 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         t[r] = r < RR ? load_chunk<ES>(geo, (w * RR + r) * 64 + l, hi) : make_uint4(0u, 0u, 0u, 0u);
     const Row R = make_row(G, gi, row, slice, rin);
     Rout = R;
+    MIS_STAMP(1);
+    MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)slice << 8) | (unsigned)R.mode);
     if (R.mode == kSkip) {
         if (slice == 0 && tid == 0 && G.tokens) gp(G.tokens)[row] = kPad;
         return kActNone;
@@ -796,6 +864,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         }
     }
     __syncthreads();
+    MIS_STAMP(2);
     // specials: counts, out of the tile, their logits loaded (the loads land during pass 1)
     const int ns = min(L.nspec, kSpecCap);
     if (tid == 0 && L.nspec > kSpecCap) L.flags |= kRecOverflow;
@@ -816,6 +885,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         }
     }
     __syncthreads();
+    MIS_STAMP(3);
 
     // pass 1: keep bits applied; lane max (and first argmax for greedy rows) in the tile's domain
     float lmax = -INFINITY;
@@ -869,6 +939,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         }
     }
 
+    MIS_STAMP(4);
     if (R.mode == kGreedy) {
         // greedy: q = x (no temperature); specials compete with their processed values
         float v = lmax;
@@ -937,6 +1008,68 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         return arrive(A, R, L) ? kActFinalize : kActNone;
     }
 
+    if constexpr (ES == 2) {
+        if (nucleus_hist(R, ES)) {
+            // the count of every value (kHistReps copies: lane l adds to copy l % kHistReps, so lanes of a wave that
+            // hold one value spread their LDS atomics over several addresses and banks; the history counts are no
+            // longer needed); the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
+            uint4* hk4 = (uint4*)L.a.cnt;
+            for (int i = tid; i < kHistReps * kHistStride / 4; i += kThreads) hk4[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (tid == 0) L.tinyfx = 0ull;
+            __syncthreads();
+            uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
+            unsigned long long tf = 0ull;
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                if (r >= RR) continue;
+                const uint32_t wv[4] = {t[r].x, t[r].y, t[r].z, t[r].w};
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
+                    if (b != 0xff80u) {
+                        const int k = bf_key(b);
+                        atomicAdd(&hk[k], 1u);
+                        if (k == kKeyZero - 1 || k == kKeyZero + 1)
+                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, __uint_as_float(b << 16))) * kFx);
+                    }
+                }
+            }
+            tf = wave_reduce(tf, [](unsigned long long a, unsigned long long b) { return a + b; });
+            if (l == 0 && tf) atomicAdd(&L.tinyfx, tf);
+            // the specials with their bins (their values are not in the counts)
+            unsigned long long* sg = (unsigned long long*)((char*)rec + kRecSpecOff);
+            uint32_t* sbin = (uint32_t*)((char*)rec + kRecSpecBinOff);
+            for (int i = tid; i < ns; i += kThreads) {
+                const float q = L.spec[i].q;
+                sg[i] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
+                        __float_as_uint(q);
+                const int b = q > -INFINITY ? hist_bin(R, q, [&](int k) { return key_q(R, k); }) : -1;
+                sbin[i] = (uint32_t)(b + 1);  // 0: below every key or -inf
+            }
+            __syncthreads();
+            uint32_t* hg = (uint32_t*)((char*)rec + kRecHistOff);
+            for (int i = tid; i < kHistWords; i += kThreads) {
+                uint32_t a = 0u, b = 0u;
+#pragma unroll
+                for (int c = 0; c < kHistReps; ++c) {
+                    a += L.a.cnt[c * kHistStride + 2 * i];
+                    b += L.a.cnt[c * kHistStride + 2 * i + 1];
+                }
+                hg[i] = a | (b << 16);
+            }
+            if (tid == 0) {
+                rec->mq = mq;
+                rec->mqd = mqd;
+                rec->gate = -INFINITY;
+                rec->flags = L.flags;
+                rec->hist = 1;
+                rec->nspec = ns;
+                rec->tinyfx = L.tinyfx;
+            }
+            return arrive(A, R, L) ? kActFinalize : kActNone;
+        }
+    }
+
     // top-k and top-p rows: per-wave gates; every element of the wave at or above its gate is published
     // the slice's gate (tile domain): a value that at least c_gate of its lane maxima reach, the c-th largest lane max
     // to within one bin of a 256-bin histogram of them over [min, max]; each wave reads the histogram itself
@@ -962,22 +1095,13 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             gate = (!binned || b <= 0) ? lo_l : lo_l + (float)(b - 1) * (span_l * (1.0f / 256.0f));
         }
     }
+    MIS_STAMP(16);
     const float gate_q = (gate > -INFINITY) ? to_q<ES>(R, gate) : -INFINITY;
     unsigned long long* segs = (unsigned long long*)((char*)rec + kRecCandOff);
     unsigned long long* myseg = segs + (int64_t)w * kCapWave;
     int cnt = 0, flags = 0;
     double zacc = 0.0, cacc = 0.0;
     const float mref = mq;
-    // bf16 top-p rows without top-k also publish the count of every value (the nucleus histogram) and their
-    // specials, which settle a nucleus wider than the candidates
-    const bool hist = ES == 2 && R.mode == kNucleus && R.T >= 0.015625f;
-    if (hist) {
-        // kHistReps copies of the counts (the history counts are no longer needed): lane l adds to copy l % kHistReps,
-        // so lanes of a wave that hold one value spread their LDS atomics over several addresses and banks
-        uint4* hk4 = (uint4*)L.a.cnt;
-        for (int i = tid; i < kHistReps * kHistStride / 4; i += kThreads) hk4[i] = make_uint4(0u, 0u, 0u, 0u);
-        if (tid == 0) L.tinyfx = 0ull;
-    }
 #pragma unroll
     for (int r = 0; r < RMAX; ++r) {
         if (r >= RR) continue;
@@ -1016,6 +1140,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             }
         }
     }
+    MIS_STAMP(17);
     // specials at or above the gate (every wave; slots of segment kWaves reserved in LDS)
     unsigned long long* sseg = segs + (int64_t)kWaves * kCapWave;
     for (int i0 = 0; i0 < ns; i0 += kThreads) {
@@ -1042,55 +1167,16 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         cacc = wave_reduce(cacc, [](double a, double b) { return a + b; });
     }
     flags = wave_reduce(flags, [](int a, int b) { return a | b; });
+    MIS_STAMP(18);
     __syncthreads();
+    MIS_STAMP(19);
     if (l == 0) {
         L.segoff[w] = cnt;
         L.red.d[w] = zacc;
         L.sb[w] = cacc;
         if (flags) atomicOr(&L.flags, flags);
     }
-    if constexpr (ES == 2) {
-        if (hist) {
-            // counts by value key; the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
-            uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
-            unsigned long long tf = 0ull;
-#pragma unroll
-            for (int r = 0; r < RMAX; ++r) {
-                if (r >= RR) continue;
-                const uint32_t wv[4] = {t[r].x, t[r].y, t[r].z, t[r].w};
-#pragma unroll
-                for (int h = 0; h < 8; ++h) {
-                    const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
-                    if (b != 0xff80u) {
-                        const int k = bf_key(b);
-                        atomicAdd(&hk[k], 1u);
-                        if (k == kKeyZero - 1 || k == kKeyZero + 1)
-                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, __uint_as_float(b << 16))) * kFx);
-                    }
-                }
-            }
-            tf = wave_reduce(tf, [](unsigned long long a, unsigned long long b) { return a + b; });
-            if (l == 0 && tf) atomicAdd(&L.tinyfx, tf);
-        }
-    }
     __syncthreads();
-    if (hist) {
-        const uint32_t* hk = L.a.cnt;
-        uint32_t* hg = (uint32_t*)((char*)rec + kRecHistOff);
-        for (int i = tid; i < kHistWords; i += kThreads) {
-            uint32_t a = 0u, b = 0u;
-#pragma unroll
-            for (int c = 0; c < kHistReps; ++c) {
-                a += hk[c * kHistStride + 2 * i];
-                b += hk[c * kHistStride + 2 * i + 1];
-            }
-            hg[i] = a | (b << 16);
-        }
-        unsigned long long* sg = (unsigned long long*)((char*)rec + kRecSpecOff);
-        for (int i = tid; i < ns; i += kThreads)
-            sg[i] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
-                    __float_as_uint(L.spec[i].q);
-    }
     if (tid == 0) {
         double z = 0.0, zc = 0.0;
 #pragma unroll
@@ -1106,9 +1192,8 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         rec->mref = mref;
         rec->z = z;
         rec->flags = L.flags | (gate_q > -INFINITY ? 0 : kRecGateInf);
-        rec->hist = hist ? 1 : 0;
+        rec->hist = 0;
         rec->nspec = ns;
-        rec->tinyfx = L.tinyfx;
     }
     if (tid < kWaves) rec->ncand[tid] = L.segoff[tid];
     return arrive(A, R, L) ? kActFinalize : kActNone;
@@ -2341,6 +2426,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
     }
     __syncthreads();
     const int n = L.segoff[nseg];
+    MIS_STAMP(26);
     if (L.token || n > kCapCand) return false;
     const float m_sel = L.fscratch[0];
     // gather, with each candidate's mass relative to the row max: four loads per thread issued together
@@ -2385,6 +2471,7 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
         atomicMax((unsigned long long*)&L.uscratch[1], (unsigned long long)kmax);
     }
     __syncthreads();
+    MIS_STAMP(27);
     const uint32_t klo = n ? (uint32_t)L.uscratch[0] : 0u, khi = n ? (uint32_t)L.uscratch[1] : 0u;
     if (n > 256) {  // a large set: the whole workgroup selects
         const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
@@ -2430,16 +2517,13 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
     const float u = tid == 0 ? row_uniform(G, R) : 0.f;
     if (w == 0) {  // lane s reads slice s's record
-        float mq = -INFINITY, mqd = -INFINITY, mr = -INFINITY;
-        double zz = 0.0;
+        float mq = -INFINITY, mqd = -INFINITY;
         int bad = 0, nsp = 0;
         unsigned long long tf = 0ull;
         if (l < S) {
             const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
             mq = pub_ld(&rec->mq);
             mqd = pub_ld(&rec->mqd);
-            mr = pub_ld(&rec->mref);
-            zz = pub_ld(&rec->z);
             bad = (!pub_ld(&rec->hist) || (pub_ld(&rec->flags) & kRecOverflow)) ? 1 : 0;
             nsp = pub_ld(&rec->nspec);
             tf = pub_ld(&rec->tinyfx);
@@ -2447,8 +2531,6 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         const float m = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
         const float md = wave_reduce(mqd, [](float a, float b) { return fmaxf(a, b); });
         const int anybad = wave_reduce(bad, [](int a, int b) { return max(a, b); });
-        const double zn = wave_reduce((mr > -INFINITY && m > -INFINITY) ? zz * exp((double)mr - (double)m) : 0.0,
-                                      [](double a, double b) { return a + b; });
         const int incl = wave_incl_scan(nsp);
         if (l < S) {
             L.segoff[l] = incl - nsp;
@@ -2458,7 +2540,6 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
             L.segoff[S] = __builtin_amdgcn_readlane(incl, 63);
             L.fscratch[0] = m;
             L.fscratch[1] = md;
-            L.dscratch[0] = zn;
             L.token = anybad;
             L.nspec = 0;
         }
@@ -2466,7 +2547,6 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     __syncthreads();
     if (L.token) return false;
     const float m = L.fscratch[0], mdraw = L.fscratch[1];
-    const double zn = L.dscratch[0] * kFx;
     const int ntot = L.segoff[S];
     out.thr = -INFINITY;
     out.mdraw = -INFINITY;
@@ -2495,6 +2575,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
             cnt[2 * i + 1] = b;
         }
     }
+    MIS_STAMP(22);
     // the value of every key (a lump takes the value of the exact key below it, so the table is monotone)
     char* const abase = (char*)&L.a;
     unsigned long long* mo = (unsigned long long*)abase;  // per key: mass of the specials strictly above its value
@@ -2509,56 +2590,37 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     __syncthreads();
     const uint32_t nlump = cnt[kKeyZero - 1] + cnt[kKeyZero + 1];
     if (cnt[kKeys - 1] != 0u) return false;  // values of 256 and above are not resolved here
-    // every special into its bin: the even bin of the exact key holding its value, or the odd bin strictly between
-    // that key and the next exact one (engine/talker_sampler.py:87-92 ranks values, so equal values share a bin)
-    auto bin_of = [&](float q) -> int {  // 2 k (value of key k) or 2 k + 1 (between); -1 below every key
-        if (!(q >= qt[1])) return -1;
-        // the largest key whose value is <= q: the bf16 value nearest q T is within a key or two of it (q is x / T
-        // rounded once for the bf16 x of an exact key, and a special lies between two such values)
-        const uint32_t yb = __float_as_uint(q * R.T);
-        int lo = min(max(bf_key((yb + 0x7fffu + ((yb >> 16) & 1u)) >> 16), 1), kKeys - 1);
-        for (int it = 0; it < 4; ++it) {
-            if (qt[lo] > q)
-                --lo;
-            else if (lo + 1 < kKeys && qt[lo + 1] <= q)
-                ++lo;
+    // every special into the bin its slice found for it: the even bin of the exact key holding its value (counted
+    // with that key), or the odd bin strictly between that key and the next exact one
+    auto spec_at = [&](int i, unsigned long long& e, int& bin) {
+        int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (L.segoff[mid] <= i)
+                lo = mid;
+            else
+                hi = mid;
         }
-        if (!(qt[lo] <= q && (lo + 1 >= kKeys || q < qt[lo + 1]))) {
-            lo = 1;
-            int hi = kKeys;  // qt[lo] <= q < qt[hi]
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (qt[mid] <= q)
-                    lo = mid;
-                else
-                    hi = mid;
-            }
-        }
-        const int k = key_exact(lo) ? lo : lo - 1;
-        return qt[k] == q ? 2 * k : 2 * k + 1;
+        const char* rb = rec_base(G, R.row, lo);
+        const int o = i - L.segoff[lo];
+        e = pub_ld((const unsigned long long*)(rb + kRecSpecOff) + o);
+        bin = (int)pub_ld((const uint32_t*)(rb + kRecSpecBinOff) + o) - 1;
     };
     for (int i0 = 0; i0 < ntot; i0 += 4 * kThreads) {
         unsigned long long e[4];
+        int bn[4];
 #pragma unroll
         for (int u4 = 0; u4 < 4; ++u4) {
             const int i = i0 + u4 * kThreads + tid;
-            int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (L.segoff[mid] <= i)
-                    lo = mid;
-                else
-                    hi = mid;
-            }
-            e[u4] = i < ntot ? pub_ld((const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) +
-                                      (i - L.segoff[lo]))
-                             : 0ull;
+            e[u4] = 0ull;
+            bn[u4] = -1;
+            if (i < ntot) spec_at(i, e[u4], bn[u4]);
         }
 #pragma unroll
         for (int u4 = 0; u4 < 4; ++u4) {
             const float q = __uint_as_float((uint32_t)e[u4]);
             if (i0 + u4 * kThreads + tid >= ntot || !(q > -INFINITY)) continue;
-            const int b = bin_of(q);
+            const int b = bn[u4];
             if (b < 0) {
                 atomicAdd(&co[0], 1u);  // below every key: ranks last, weighs nothing at these magnitudes
             } else if (b & 1) {
@@ -2569,6 +2631,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
             }
         }
     }
+    MIS_STAMP(23);
     unsigned long long tiny0 = 0ull;
     for (int s = 0; s < S; ++s) tiny0 += L.slice_u[s];
     const unsigned long long lump_m = nlump ? (unsigned long long)((double)tiny0 * exp(-(double)m)) : 0ull;
@@ -2582,9 +2645,10 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     // their order is not resolved here
     auto near_lump = [&](int k) { return k == 0 || (nlump && k >= kKeyZero - 2 && k <= kKeyZero + 1); };
     // one descending pass over the keys: thread t holds keys kKeys - 1 - 4 t .. - 3; the first bin (odd bin of k,
-    // then its even bin) at which the cumulative weight reaches T; false when the total is below T
-    auto scan_cut = [&](unsigned long long T, bool by_mass, int& key_out, bool& odd_out,
-                        unsigned long long& before_out) -> bool {
+    // then its even bin) at which the cumulative weight reaches T (T0, or with frac > 0 the target ceil(frac * total),
+    // at least 1); false when the total is below T
+    auto scan_cut = [&](unsigned long long T0, double frac, bool by_mass, int& key_out, bool& odd_out,
+                        unsigned long long& before_out, unsigned long long& T_out) -> bool {
         unsigned long long wsum = 0ull;
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -2593,6 +2657,12 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         }
         unsigned long long tot;
         const unsigned long long ex = block_excl_scan(wsum, tot, L.red.u);
+        unsigned long long T = T0;
+        if (frac > 0.0) {
+            const double pt = ceil(frac * (double)tot);
+            T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+        }
+        T_out = T;
         if (tid == 0) L.token = -1;
         __syncthreads();
         if (ex < T && T <= ex + wsum) {
@@ -2636,19 +2706,13 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         for (int i0 = 0; i0 < ntot; i0 += kThreads) {
             const int i = i0 + tid;
             float q = -INFINITY;
+            int b = -1;
             if (i < ntot) {
-                int lo = 0, hi = S;
-                while (hi - lo > 1) {
-                    const int mid = (lo + hi) >> 1;
-                    if (L.segoff[mid] <= i)
-                        lo = mid;
-                    else
-                        hi = mid;
-                }
-                q = __uint_as_float((uint32_t)pub_ld(
-                    (const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) + (i - L.segoff[lo])));
+                unsigned long long e;
+                spec_at(i, e, b);
+                q = __uint_as_float((uint32_t)e);
             }
-            const bool in = q > -INFINITY && bin_of(q) == 2 * k + 1;
+            const bool in = q > -INFINITY && b == 2 * k + 1;
             const int slot = lds_reserve(in, &L.scnt);
             if (in && slot < 256) {
                 rq[slot] = q;
@@ -2684,19 +2748,19 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         __syncthreads();
         return r;
     };
-    // the top-p cut (engine/talker_sampler.py:87-92 through fixed-point masses) and the min_keep floor
-    const double pt = ceil((double)R.top_p * zn);
-    const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+    // the top-p cut (engine/talker_sampler.py:87-92 through fixed-point masses: the target is top_p of the total
+    // mass of every value in the row) and the min_keep floor
     int ck;
     bool codd;
-    unsigned long long cbef;
-    if (!scan_cut(T, true, ck, codd, cbef)) return false;
+    unsigned long long cbef, T, Tk;
+    MIS_STAMP(12);
+    if (!scan_cut(0ull, (double)R.top_p, true, ck, codd, cbef, T)) return false;
     if (near_lump(ck)) return false;
     const float thr_p = codd ? resolve_odd(ck, T, cbef, true) : qt[ck];
     if (!(thr_p == thr_p)) return false;
     float vmk = m;
     if (R.min_keep_eff >= 2) {
-        if (scan_cut((unsigned long long)R.min_keep_eff, false, ck, codd, cbef)) {
+        if (scan_cut((unsigned long long)R.min_keep_eff, 0.0, false, ck, codd, cbef, Tk)) {
             if (near_lump(ck)) return false;
             vmk = codd ? resolve_odd(ck, (unsigned long long)R.min_keep_eff, cbef, false) : qt[ck];
             if (!(vmk == vmk)) return false;
@@ -2720,6 +2784,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         }
         lut[k] = e;
     }
+    MIS_STAMP(13);
     const bool lump_surv = nlump && thr <= q_tlo;
     if (tid < S) L.sbfx[tid] = lump_surv ? (unsigned long long)((double)L.slice_u[tid] * exp(-(double)md)) : 0ull;
     __syncthreads();
@@ -2808,6 +2873,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     __syncthreads();
     const int ss = L.is_last;
     const unsigned long long rem = L.uscratch[0];
+    MIS_STAMP(14);
     if (ss < 0) return true;
     // the draw inside slice ss in one pass over it: thread t owns chunks [t nc, (t + 1) nc) (8 elements each, from
     // the slice's 16-byte aligned start) and sums their survivor masses (the specials from their list, added to
@@ -2883,11 +2949,13 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
             for (int h = 0; h < 8; ++h) acc += ((kb >> h) & 1u) ? mv[h] : 0ull;
         }
     }
+    MIS_STAMP(24);
     const unsigned long long mine = tsum[tid] + acc;
     unsigned long long tot;
     const unsigned long long ex = block_excl_scan(mine, tot, L.red.u);
     if (tid == 0) L.token = -1;
     __syncthreads();
+    MIS_STAMP(25);
     if (mine && ex < rem && rem <= ex + mine) {
         L.token = tid;
         L.uscratch[1] = rem - ex;
@@ -3099,6 +3167,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
     o.thr = -INFINITY;
     o.mdraw = -INFINITY;
     int path = MIS_PATH_FORCED;
+    MIS_STAMP(7);
     if (!forced) {
         int mode = L.foreign ? kStream : R.mode;
         if (mode == kGreedy) {
@@ -3107,21 +3176,27 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
         } else if (mode == kFull) {
             fin_full(G, R, L, o);
             path = MIS_PATH_FULL;
+        } else if (mode == kNucleus && nucleus_hist(R, G.es)) {
+            path = MIS_PATH_HISTOGRAM;
+            if (!fin_hist(G, R, L, o)) mode = kStream;
+            MIS_STAMP(9);
         } else if (mode == kTopK || mode == kNucleus) {
             path = MIS_PATH_CANDIDATES;
-            if (!fin_cands(G, R, L, o)) {
-                path = MIS_PATH_HISTOGRAM;
-                if (!(mode == kNucleus && G.es == 2 && fin_hist(G, R, L, o))) mode = kStream;
-            }
+            if (!fin_cands(G, R, L, o)) mode = kStream;
+            MIS_STAMP(8);
         }
         if (mode == kStream) {
             fin_stream(G, R, L, o);
             path = MIS_PATH_STREAM;
+            MIS_STAMP(10);
         }
     }
     if (threadIdx.x == 0 && G.paths) atomicAdd(G.paths + path, 1u);
     if (R.want_out) write_outputs(G, R, L, o, forced);
     update_state(G, R, o.token);
+    MIS_STAMP(11);
+    MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)R.slice << 8) | 0x80u |
+                   (unsigned)path);
 }
 
 __device__ __forceinline__ bool locate(const KernelArgs& A, int& gi, int& row, int& slice) {
@@ -3142,6 +3217,7 @@ __device__ __forceinline__ bool locate(const KernelArgs& A, int& gi, int& row, i
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(const KernelArgs args) {
     (void)args;
+    MIS_STAMP(0);
     // the arguments read in place from the kernarg segment: a by-value copy indexed by group would live in scratch
     const KernelArgs& A = *(const KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
     __shared__ Lds L;
@@ -3418,6 +3494,20 @@ int mis_sample_static(const MisGroup* groups, int n_groups, void* stream) {
     if (int rc = static_workspace(&ws)) return rc;
     return mis_sample(groups, n_groups, ws, kStaticWsBytes, stream);
 }
+
+#ifdef MIS_PHASE_STAMPS
+// The phase timestamps of the last launches (profiling builds only): kStampBlocks x kStampSlots words.
+int mis_debug_stamps(void* host, size_t bytes) {
+    const size_t n = std::min(bytes, sizeof(mis_stamps));
+    const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(mis_stamps), n, 0, hipMemcpyDeviceToHost);
+    return e == hipSuccess ? 0 : -1;
+}
+int mis_debug_clear_stamps(void) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(mis_stamps)) != hipSuccess) return -1;
+    return hipMemset(p, 0, sizeof(mis_stamps)) == hipSuccess ? 0 : -1;
+}
+#endif
 
 int mis_uniform(const int64_t* seeds, const int64_t* steps, const int64_t* row_ids, int64_t n, int32_t rng, float* out,
                 void* stream) {
