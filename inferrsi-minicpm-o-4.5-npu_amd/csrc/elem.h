@@ -66,8 +66,16 @@ __host__ __device__ __forceinline__ float philox_uniform(int64_t seed, int64_t s
 // product may fall on either side: a result under 2^-125 in magnitude is therefore recomputed by IEEE division.
 // Infinities, zeros (with their sign) and NaN pass through as IEEE division has them.
 __device__ __forceinline__ float div_rn(float x, float d, double rd) {
-    const float q = (float)((double)x * rd);
-    return (fabsf(q) < 0x1p-125f && x != 0.0f) ? x / d : q;
+    float q = (float)((double)x * rd);
+    const bool tiny = fabsf(q) < 0x1p-125f && x != 0.0f;
+    // a branch on the wave, not a select: the IEEE division runs only when some lane needs it (the empty asm
+    // keeps the compiler from computing it ahead of the branch)
+    if (__builtin_amdgcn_ballot_w64(tiny)) {
+        float xs = x;
+        asm volatile("" : "+v"(xs));
+        if (tiny) q = xs / d;
+    }
+    return q;
 }
 
 // exp(x) within ~1.3 ulp: 2^(x log2 e) with the product's rounding error (and log2 e's own) folded back in

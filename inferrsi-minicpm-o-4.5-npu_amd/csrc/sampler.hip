@@ -155,7 +155,7 @@ struct SliceRec {
     double z;        // sum of exp(q - mref) (whole-vocabulary normaliser)
     double zc;       // the part of z over the published candidates
     int32_t ncand[kSegs];
-    int32_t pad0;
+    int32_t nhigh;   // histogram path: the first nhigh published specials lie at or above the value gate
     unsigned long long tinyfx;  // sum of exp(q) in fixed point over the tiny-magnitude lumps of the histogram
 };
 constexpr int64_t kRecHead = 256;
@@ -198,6 +198,18 @@ struct SmallSet {
     unsigned long long mass[kCapSmall];
 };
 
+constexpr int kSelBins = kBins;  // value bins of the candidate finaliser (their masses live in Hist::w)
+constexpr int kSelCap = 1024;    // elements of one bin ranked exactly; specials of a row drawn from
+
+// Candidate finaliser: bin counts, one bin ranked (compacted, then sorted), the specials in id order.
+struct SelScratch {
+    uint32_t bcnt[kSelBins];
+    float cq[kSelCap];
+    unsigned long long cw[kSelCap];
+    float sq[kSelCap];
+    unsigned long long sw[kSelCap];
+};
+
 // LDS of one workgroup.  The slice phase and the finaliser overlay the big arrays.
 struct Lds {
     union {
@@ -217,6 +229,7 @@ struct Lds {
     union {
         Special spec[kSpecCap];  // slice phase
         SmallSet sm[2];          // finaliser: narrowed candidate sets (compaction alternates between the two)
+        SelScratch ss;           // finaliser: the candidate selection
     };
     double sb[kMaxSB];
     unsigned long long sbfx[kMaxSB];
@@ -227,6 +240,7 @@ struct Lds {
     int32_t scnt;
     int32_t flags;
     int32_t is_last;
+    int32_t nhi, nlo;  // slice phase of the histogram path: specials at or above the value gate, and below it
     int32_t foreign;
     int32_t token;
     float fscratch[4];
@@ -234,6 +248,7 @@ struct Lds {
     unsigned long long tinyfx;               // slice phase: the histogram's tiny lumps
     unsigned long long uscratch[2];
     unsigned long long slice_u[kMaxSlices];  // finaliser: per-slice sums
+    int32_t slice_n[kMaxSlices];             // finaliser (histogram path): specials each slice published
 };
 static_assert(sizeof(Lds) <= 160 * 1024, "LDS budget");
 
@@ -1010,15 +1025,34 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
 
     if constexpr (ES == 2) {
         if (nucleus_hist(R, ES)) {
-            // the count of every value (kHistReps copies: lane l adds to copy l % kHistReps, so lanes of a wave that
-            // hold one value spread their LDS atomics over several addresses and banks; the history counts are no
-            // longer needed); the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
+            // the count of every value at or above a value gate (the nucleus histogram), and the summed mass of the
+            // values below it: the values below mq - D weigh at most V e^-D of the row's largest, less than the
+            // 1 - top_p of the row the cut leaves below it, so the cut lies above them whenever the row's largest
+            // is in the slice; the finaliser checks that its cut lies above every slice's bound hb and streams the
+            // row otherwise
+            const float D = R.top_p < 1.0f ? __logf((float)R.V) - log1pf(-R.top_p) + 2.0f : INFINITY;
+            const float gate_q = mq - D;
+            const float g_raw = gate_q * R.T;  // tile domain: x >= g_raw is counted
+            const float hb = fmaxf(to_q<2>(R, g_raw), gate_q);  // every value left out is <= hb
+            // kHistReps copies of the counts (lane l adds to copy l % kHistReps, so lanes of a wave that hold one
+            // value spread their LDS atomics over several addresses and banks; the history counts are no longer
+            // needed); the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
             uint4* hk4 = (uint4*)L.a.cnt;
             for (int i = tid; i < kHistReps * kHistStride / 4; i += kThreads) hk4[i] = make_uint4(0u, 0u, 0u, 0u);
-            if (tid == 0) L.tinyfx = 0ull;
+            if (tid == 0) {
+                L.tinyfx = 0ull;
+                L.nhi = 0;
+                L.nlo = 0;
+            }
             __syncthreads();
+            MIS_STAMP(26);
             uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
             unsigned long long tf = 0ull;
+            // sum of exp(q - mq) over what is left out, as 2^(x log2(e) / T - mq log2(e)) in float: these masses
+            // sum to at most V e^-D of the row's largest, so their relative error of a few 1e-6 stays far below
+            // the counts' fixed-point resolution of the total
+            const float c1 = (float)(1.4426950408889634 / (double)R.T), c2 = mq * 1.44269502f;
+            float zr = 0.0f;
 #pragma unroll
             for (int r = 0; r < RMAX; ++r) {
                 if (r >= RR) continue;
@@ -1026,27 +1060,45 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
 #pragma unroll
                 for (int h = 0; h < 8; ++h) {
                     const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
-                    if (b != 0xff80u) {
+                    const float x = __uint_as_float(b << 16);
+                    if (b == 0xff80u) continue;
+                    if (x >= g_raw) {
                         const int k = bf_key(b);
                         atomicAdd(&hk[k], 1u);
                         if (k == kKeyZero - 1 || k == kKeyZero + 1)
-                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, __uint_as_float(b << 16))) * kFx);
+                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, x)) * kFx);
+                    } else if (x == x) {
+                        zr += __builtin_amdgcn_exp2f(__builtin_fmaf(x, c1, -c2));
                     }
                 }
             }
             tf = wave_reduce(tf, [](unsigned long long a, unsigned long long b) { return a + b; });
             if (l == 0 && tf) atomicAdd(&L.tinyfx, tf);
-            // the specials with their bins (their values are not in the counts)
+            MIS_STAMP(27);
+            // the specials with their bins, those at or above the gate first (their values are not in the counts;
+            // the ones below the gate are listed only for the draw's pass over the slice)
             unsigned long long* sg = (unsigned long long*)((char*)rec + kRecSpecOff);
             uint32_t* sbin = (uint32_t*)((char*)rec + kRecSpecBinOff);
-            for (int i = tid; i < ns; i += kThreads) {
-                const float q = L.spec[i].q;
-                sg[i] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
-                        __float_as_uint(q);
-                const int b = q > -INFINITY ? hist_bin(R, q, [&](int k) { return key_q(R, k); }) : -1;
-                sbin[i] = (uint32_t)(b + 1);  // 0: below every key or -inf
+            for (int i0 = 0; i0 < ns; i0 += kThreads) {
+                const int i = i0 + tid;
+                const float q = i < ns ? L.spec[i].q : -INFINITY;
+                const bool high = i < ns && q > -INFINITY && q >= gate_q;
+                const bool low = i < ns && !high;
+                const int sh = lds_reserve(high, &L.nhi);
+                const int sl = lds_reserve(low, &L.nlo);
+                if (i < ns) {
+                    const int slot = high ? sh : ns - 1 - sl;
+                    sg[slot] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
+                               __float_as_uint(q);
+                    const int b = high ? hist_bin(R, q, [&](int k) { return key_q(R, k); }) : -1;
+                    sbin[slot] = (uint32_t)(b + 1);  // 0: below every key or -inf
+                    if (low && q > -INFINITY) zr += exp_acc(q - mq);
+                }
             }
+            const double zrd = wave_reduce((double)zr, [](double a, double b) { return a + b; });
+            if (l == 0) L.red.d[w] = zrd;
             __syncthreads();
+            MIS_STAMP(28);
             uint32_t* hg = (uint32_t*)((char*)rec + kRecHistOff);
             for (int i = tid; i < kHistWords; i += kThreads) {
                 uint32_t a = 0u, b = 0u;
@@ -1057,13 +1109,20 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 }
                 hg[i] = a | (b << 16);
             }
+            MIS_STAMP(29);
             if (tid == 0) {
+                double z = 0.0;
+#pragma unroll
+                for (int i = 0; i < kWaves; ++i) z += L.red.d[i];
                 rec->mq = mq;
                 rec->mqd = mqd;
-                rec->gate = -INFINITY;
+                rec->gate = hb;
+                rec->mref = mq;
+                rec->z = z;
                 rec->flags = L.flags;
                 rec->hist = 1;
                 rec->nspec = ns;
+                rec->nhigh = L.nhi;
                 rec->tinyfx = L.tinyfx;
             }
             return arrive(A, R, L) ? kActFinalize : kActNone;
@@ -2508,6 +2567,497 @@ __device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& 
     return true;
 }
 
+// ------------------------------------------------------------------ the candidate finaliser (whole workgroup)
+//
+// The row's candidates (every element at or above its slice's gate, and the slices' specials at or above it) are
+// gathered into LDS: the tile candidates first, in token order (slices in order, each slice's waves in order), then
+// the specials.  Each question of the selection (the k-th value, the top-p cut, the min_keep floor) is one block
+// scan over kSelBins value bins filled by one pass of LDS atomics; only the bin that holds the answer is ranked
+// element by element, by every thread at once.  The draw is one block scan in token order.
+
+// Value bins over [qmin, qmax]: monotone in the value, equal values share a bin.
+struct SelBins {
+    float qmin, scale;
+};
+__device__ __forceinline__ int sel_bin(float q, const SelBins& B) {
+    const float f = fminf((q - B.qmin) * B.scale, (float)(kSelBins - 1));
+    return max((int)f, 0);
+}
+
+// The bin at which the cumulative weight wt(b), taken from the highest bin down, first reaches T >= 1; `before` = the
+// weight of the bins above it, `total` = all of it.  -1 when the total is below T.  Every thread gets the result.
+template <class WT>
+__device__ __forceinline__ int sel_find_bin(WT&& wt, unsigned long long T, unsigned long long& before,
+                                            unsigned long long& total, Lds& L) {
+    const int tid = threadIdx.x;
+    const int b0 = kSelBins - 1 - 2 * tid, b1 = b0 - 1;
+    const unsigned long long w0 = wt(b0), w1 = wt(b1);
+    const unsigned long long mine = w0 + w1;
+    const unsigned long long ex = block_excl_scan(mine, total, L.red.u);
+    if (tid == 0) L.token = -1;
+    __syncthreads();
+    if (ex < T && T <= ex + mine) {
+        const bool first = ex + w0 >= T;
+        L.token = first ? b0 : b1;
+        L.uscratch[1] = first ? ex : ex + w0;
+    }
+    __syncthreads();
+    const int b = L.token;
+    before = L.uscratch[1];
+    __syncthreads();
+    return b;
+}
+
+// The elements of bin b sorted by value, descending (equal values in any order: they weigh alike): values in
+// L.ss.sq, set indices in L.ss.sw; returns their count, or -1 when more than kSelCap.
+__device__ __forceinline__ int sel_sort_bin(int b, int n, const SelBins& B, Lds& L) {
+    const int tid = threadIdx.x;
+    if (tid == 0) L.scnt = 0;
+    __syncthreads();
+    for (int i0 = 0; i0 < n; i0 += kThreads) {
+        const int i = i0 + tid;
+        const float q = i < n ? L.a.w.q[i] : 0.f;
+        const bool in = i < n && sel_bin(q, B) == b;
+        const int slot = lds_reserve(in, &L.scnt);
+        if (in && slot < kSelCap) {
+            L.ss.cq[slot] = q;
+            L.ss.cw[slot] = (unsigned long long)i;
+        }
+    }
+    __syncthreads();
+    MIS_STAMP(23);
+    const int m = L.scnt;
+    if (m > kSelCap) return -1;
+    // a bin of one value (the usual case: the bins are finer than the values' spacing) is sorted as it stands
+    if (tid == 0) L.flags = 0;
+    __syncthreads();
+    if (tid < m && L.ss.cq[tid] != L.ss.cq[0]) L.flags = 1;
+    __syncthreads();
+    if (L.flags == 0) {
+        if (tid < m) {
+            L.ss.sq[tid] = L.ss.cq[tid];
+            L.ss.sw[tid] = L.ss.cw[tid];
+        }
+        __syncthreads();
+        return m;
+    }
+    if (tid < m) {
+        const float q = L.ss.cq[tid];
+        const uint32_t k = ord_key(q);
+        int r = 0;
+        // eight values per step, read together (the reads are broadcasts; one step waits once)
+        for (int j0 = 0; j0 < m; j0 += 8) {
+            float c[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) c[e] = L.ss.cq[min(j0 + e, m - 1)];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int j = j0 + e;
+                const uint32_t kj = ord_key(c[e]);
+                r += (j < m && (kj > k || (kj == k && j < tid))) ? 1 : 0;
+            }
+        }
+        L.ss.sq[r] = q;
+        L.ss.sw[r] = L.ss.cw[tid];
+    }
+    __syncthreads();
+    return m;
+}
+
+// Position in the sorted bin (m elements) at which `before` plus the cumulative weight first reaches T; -1 if never.
+__device__ __forceinline__ int sel_cross(int m, unsigned long long before, unsigned long long T, Lds& L) {
+    const int tid = threadIdx.x;
+    const unsigned long long w = tid < m ? L.ss.sw[tid] : 0ull;
+    unsigned long long tot;
+    const unsigned long long ex = block_excl_scan(w, tot, L.red.u) + before;
+    if (tid == 0) L.token = -1;
+    __syncthreads();
+    if (tid < m && w && ex < T && T <= ex + w) L.token = tid;
+    __syncthreads();
+    const int r = L.token;
+    __syncthreads();
+    return r;
+}
+
+// The value at descending rank r (0-based) of the set (the k-th value, the min_keep floor), NaN if unresolved; its
+// bin stays sorted in L.ss (m elements), `above` = how many elements of the set exceed the value, f = the first
+// position of the value in the sorted bin.
+__device__ __forceinline__ float sel_rank_value(int r, int n, const SelBins& B, Lds& L, int& m, int& f,
+                                                unsigned long long& above) {
+    unsigned long long before, tot;
+    const uint32_t* bc = L.ss.bcnt;
+    const int b = sel_find_bin([&](int x) { return (unsigned long long)bc[x]; }, (unsigned long long)r + 1ull,
+                               before, tot, L);
+    m = -1;
+    MIS_STAMP(22);
+    if (b < 0) return __uint_as_float(0x7fc00000u);
+    m = sel_sort_bin(b, n, B, L);
+    MIS_STAMP(24);
+    if (m < 0) return __uint_as_float(0x7fc00000u);
+    const int p = (int)((unsigned long long)r - before);
+    if (p >= m) return __uint_as_float(0x7fc00000u);
+    const float v = L.ss.sq[p];
+    int lo = 0, hi = p;  // first position of v (the bin is sorted, descending)
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (L.ss.sq[mid] > v)
+            lo = mid + 1;
+        else
+            hi = mid;
+    }
+    f = lo;
+    above = before + (unsigned long long)f;
+    return v;
+}
+
+__device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
+    const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
+    const int ntile = S * kWaves, nseg = ntile + S;  // tile segments (slice-major), then one specials segment per slice
+    if (w == 0) {
+        // records (lane s: slice s) and segment counts (lane l: segments [l * per, (l + 1) * per)); the draw's
+        // uniform after their loads are issued
+        float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
+        double zz = 0.0, zcc = 0.0;
+        int over = 0, notinf = 0;
+        if (l < S) {
+            const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
+            mq = pub_ld(&rec->mq);
+            gt = pub_ld(&rec->gate);
+            mr = pub_ld(&rec->mref);
+            zz = pub_ld(&rec->z);
+            zcc = pub_ld(&rec->zc);
+            const int fl = pub_ld(&rec->flags);
+            over = (fl & kRecOverflow) ? 1 : 0;
+            notinf = (fl & kRecGateInf) ? 0 : 1;
+        }
+        const int per = (nseg + 63) >> 6;
+        int c[kSegs];
+        int mine = 0;
+#pragma unroll
+        for (int t = 0; t < kSegs; ++t) {
+            const int i = l * per + t;
+            int v = 0;
+            if (t < per && i < nseg) {
+                const int s = i < ntile ? i / kWaves : i - ntile;
+                const int sg = i < ntile ? i % kWaves : kWaves;
+                v = pub_ld(&((const SliceRec*)rec_base(G, R.row, s))->ncand[sg]);
+            }
+            c[t] = v;
+            mine += v;
+        }
+        const float u = row_uniform(G, R);
+        const float m_sel = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
+        const float gate = wave_reduce(gt, [](float a, float b) { return fmaxf(a, b); });
+        const float gmin = wave_reduce(l < S ? gt : INFINITY, [](float a, float b) { return fminf(a, b); });
+        const int anyover = wave_reduce(over, [](int a, int b) { return max(a, b); });
+        const int anyfin = wave_reduce(notinf, [](int a, int b) { return max(a, b); });
+        double zs = 0.0, zcs = 0.0;
+        if (R.needz) {
+            const double sc = (mr > -INFINITY && m_sel > -INFINITY) ? exp((double)mr - (double)m_sel) : 0.0;
+            zs = wave_sum(zz * sc);
+            zcs = wave_sum(zcc * sc);
+        }
+        // a top-p row without top-k whose candidates weigh clearly less than top_p of the row cannot be cut among
+        // them
+        const int short_mass = (R.mode == kNucleus && R.p_active && zcs < (double)R.top_p * zs * (1.0 - 1e-6)) ? 1 : 0;
+        const int incl = wave_incl_scan(mine);
+        int o = incl - mine;
+#pragma unroll
+        for (int t = 0; t < kSegs; ++t) {
+            const int i = l * per + t;
+            if (t < per && i < nseg) L.segoff[i] = o;
+            o += c[t];
+        }
+        if (l == 0) {
+            L.segoff[nseg] = __builtin_amdgcn_readlane(incl, 63);
+            L.fscratch[0] = m_sel;
+            L.fscratch[1] = gate;
+            L.fscratch[2] = u;
+            L.fscratch[3] = gmin;
+            L.dscratch[0] = zs;
+            L.token = anyover | short_mass;
+            L.is_last = anyfin;
+        }
+    }
+    __syncthreads();
+    MIS_STAMP(26);
+    const int n = L.segoff[nseg], na = L.segoff[ntile];
+    const bool ginf = L.is_last == 0;  // every slice published all its finite elements
+    if (L.token || n > kCapCand || n - na > kSelCap) return false;
+    const float m_sel = L.fscratch[0], gate = L.fscratch[1], u = L.fscratch[2];
+    const double zfull_fx = L.dscratch[0] * kFx;
+    out.thr = -INFINITY;
+    out.mdraw = -INFINITY;
+    out.token = R.V - 1;
+    if (n == 0) return ginf;
+    // gather: every load issued at once (at most kCapCand / kThreads per thread), each candidate with its mass
+    // relative to the row max
+    constexpr int kPer = kCapCand / kThreads;
+    unsigned long long v[kPer];
+#pragma unroll
+    for (int u4 = 0; u4 < kPer; ++u4) {
+        const int i = u4 * kThreads + tid;
+        v[u4] = 0ull;
+        if (i < n) {
+            int lo = 0, hi = nseg;  // segment: segoff[lo] <= i < segoff[lo + 1]
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (L.segoff[mid] <= i)
+                    lo = mid;
+                else
+                    hi = mid;
+            }
+            const int s = lo < ntile ? lo / kWaves : lo - ntile;
+            const int sg = lo < ntile ? lo % kWaves : kWaves;
+            const unsigned long long* seg =
+                (const unsigned long long*)(rec_base(G, R.row, s) + kRecCandOff) + (int64_t)sg * kCapWave;
+            v[u4] = pub_ld(seg + (i - L.segoff[lo]));
+        }
+    }
+    // every candidate lies in [min gate, m_sel] (a slice with no gate published all its finite values: then the
+    // range comes from the values)
+    float qlo = L.fscratch[3], qhi = m_sel;
+    const bool need_lo = !(qlo > -INFINITY);
+    float vlo = INFINITY;
+#pragma unroll
+    for (int u4 = 0; u4 < kPer; ++u4) {
+        const int i = u4 * kThreads + tid;
+        if (i >= n) continue;
+        const float q = __uint_as_float((uint32_t)v[u4]);
+        L.a.w.q[i] = q;
+        L.a.w.id[i] = (uint32_t)(v[u4] >> 32);
+        L.a.w.mass[i] = efx(q, m_sel);
+        vlo = fminf(vlo, q);
+    }
+    if (need_lo) qlo = -block_max4(make_float4(-vlo, -INFINITY, -INFINITY, -INFINITY), L.red).x;
+    MIS_STAMP(27);
+    SelBins B;
+    B.qmin = qlo;
+    B.scale = qhi > qlo ? fminf((float)kSelBins / (qhi - qlo), 1e30f) : 0.0f;
+    // counts and masses by bin
+    uint32_t* bc = L.ss.bcnt;
+    unsigned long long* bm = L.h.w;
+    for (int b = tid; b < kSelBins; b += kThreads) {
+        bc[b] = 0u;
+        bm[b] = 0ull;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u4 = 0; u4 < kPer; ++u4) {
+        const int i = u4 * kThreads + tid;
+        if (i >= n) continue;
+        const float q = __uint_as_float((uint32_t)v[u4]);
+        const int b = sel_bin(q, B);
+        atomicAdd(&bc[b], 1u);
+        const unsigned long long ms = efx(q, m_sel);
+        if (ms) atomicAdd(&bm[b], ms);
+    }
+    __syncthreads();
+    MIS_STAMP(16);
+    const bool topk = R.kk < R.V;
+    // the k-th value (engine/talker_sampler.py:95-98, :119-133): ties at it count once per rank
+    float kth = -INFINITY;
+    unsigned long long cnt_gt = (unsigned long long)n;
+    int bk = -1, mk = 0, fk = 0;
+    if (topk) {
+        if (R.kk <= n) {
+            kth = sel_rank_value(R.kk - 1, n, B, L, mk, fk, cnt_gt);
+            if (!(kth >= gate)) return false;  // NaN (unresolved) included
+            bk = sel_bin(kth, B);              // its sorted elements stay in L.ss
+        } else if (!ginf) {
+            return false;
+        }
+    }
+    MIS_STAMP(17);
+    float thr = kth;
+    if (R.p_active) {
+        // weights: the mass of every value above kth, and kk - cnt_gt copies of kth's at its first rank (the ranks
+        // it fills)
+        const unsigned long long ekth = efx(kth, m_sel);
+        const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
+        unsigned long long gtk = 0ull;  // bin bk's mass above kth: its first fk sorted elements
+        if (bk >= 0) {
+            unsigned long long mine = 0ull;
+            if (tid < fk) mine = L.a.w.mass[(int)L.ss.sw[tid]];
+            gtk = block_sum_u(mine, L.red);
+        }
+        auto wt = [&](int b) -> unsigned long long {
+            if (bk < 0 || b > bk) return bm[b];
+            return b == bk ? gtk + vw : 0ull;
+        };
+        // the normaliser: the top-k mass (omni order with top-k), else the whole row's
+        double zn;
+        if (topk && !R.hf) {
+            unsigned long long t2 = 0ull;
+            for (int b = tid; b < kSelBins; b += kThreads) t2 += wt(b);
+            zn = (double)block_sum_u(t2, L.red);
+        } else {
+            zn = zfull_fx;
+        }
+        const double pt = ceil((double)R.top_p * zn);
+        const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
+        unsigned long long before, tot;
+        const int bp = sel_find_bin(wt, T, before, tot, L);
+        float thr_p;
+        if (bp >= 0) {
+            // the bin's elements by value with their weights (bin bk is sorted already)
+            const int m = bp == bk ? mk : sel_sort_bin(bp, n, B, L);
+            if (m < 0) return false;
+            if (tid < m) {
+                const int i = (int)L.ss.sw[tid];
+                unsigned long long wgt = L.ss.sq[tid] > kth ? L.a.w.mass[i] : 0ull;
+                if (bp == bk && tid == fk) wgt += vw;
+                L.ss.sw[tid] = wgt;
+            }
+            const int r = sel_cross(m, before, T, L);  // its first barrier publishes the weights
+            if (r < 0) return false;
+            thr_p = L.ss.sq[r];
+        } else {
+            if (!topk) return false;  // the nucleus reaches below the candidates
+            thr_p = kth;
+        }
+        if (!topk && !(thr_p >= gate)) return false;
+        MIS_STAMP(18);
+        float vmk = m_sel;
+        if (R.min_keep_eff >= 2) {
+            if (R.min_keep_eff > n) {
+                vmk = -INFINITY;
+            } else {
+                int m2, f2;
+                unsigned long long a2;
+                vmk = sel_rank_value(R.min_keep_eff - 1, n, B, L, m2, f2, a2);
+                if (!(vmk >= gate)) return false;
+            }
+        }
+        thr = fminf(thr_p, vmk);
+        if (topk) thr = fmaxf(thr, kth);
+    }
+    MIS_STAMP(19);
+    // survivors: drawable, q >= thr; masses relative to the largest of them
+    const uint32_t thrkey = ord_key(thr);
+    float md = -INFINITY;
+    for (int i = tid; i < n; i += kThreads) {
+        const float q = L.a.w.q[i];
+        if (ord_key(q) >= thrkey && !(L.a.w.id[i] & kSelOnlyBit)) md = fmaxf(md, q);
+    }
+    md = block_max4(make_float4(md, -INFINITY, -INFINITY, -INFINITY), L.red).x;
+    out.thr = thr;
+    out.mdraw = md;
+    if (!(md > -INFINITY)) return true;
+    const bool md_is_m = md == m_sel;
+    auto wsurv = [&](int i) -> unsigned long long {
+        const float q = L.a.w.q[i];
+        if (!(ord_key(q) >= thrkey) || (L.a.w.id[i] & kSelOnlyBit)) return 0ull;
+        return md_is_m ? L.a.w.mass[i] : efx(q, md);
+    };
+    // the draw (engine/talker_sampler.py:161-172) in token order: the specials (ids in their slices' ranges, in any
+    // order) are ranked by id and summed in that order; thread t then walks tile candidates [t c, (t + 1) c) with
+    // the specials below each id found by binary search, and leaves the tile's running sum in place of the masses
+    // for the specials' own search
+    MIS_STAMP(20);
+    const int nb = n - na;
+    uint32_t* bids = (uint32_t*)L.ss.cq;  // the surviving specials' ids, ascending
+    unsigned long long* bpre = L.ss.cw;  // inclusive sums of their masses in that order
+    // the specials that survive (few), ranked by id
+    const unsigned long long wsp = tid < nb ? wsurv(na + tid) : 0ull;
+    const uint32_t sid = tid < nb ? (L.a.w.id[na + tid] & ~kSelOnlyBit) : 0u;
+    if (tid == 0) L.scnt = 0;
+    __syncthreads();
+    const int slot = lds_reserve(wsp != 0ull, &L.scnt);
+    if (wsp) {
+        L.ss.bcnt[slot] = sid;
+        L.ss.sw[slot] = wsp;
+    }
+    __syncthreads();
+    const int nbs = L.scnt;
+    uint32_t myid = 0u;
+    unsigned long long myw = 0ull;
+    int myr = -1;
+    if (tid < nbs) {
+        myid = L.ss.bcnt[tid];
+        myw = L.ss.sw[tid];
+        int r = 0;
+        for (int j0 = 0; j0 < nbs; j0 += 8) {  // ids are distinct; eight read together
+            uint32_t c[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) c[e] = L.ss.bcnt[min(j0 + e, nbs - 1)];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r += (j0 + e < nbs && c[e] < myid) ? 1 : 0;
+        }
+        myr = r;
+        bids[r] = myid;
+    }
+    __syncthreads();
+    if (myr >= 0) L.ss.sw[myr] = myw;
+    __syncthreads();
+    const unsigned long long wsorted = tid < nbs ? L.ss.sw[tid] : 0ull;
+    unsigned long long zsb, zsa;
+    const unsigned long long exb = block_excl_scan(wsorted, zsb, L.red.u);
+    if (tid < nbs) bpre[tid] = exb + wsorted;
+    const int cpt = (na + kThreads - 1) / kThreads;
+    unsigned long long own = 0ull;
+    for (int j = 0; j < cpt; ++j) {
+        const int i = tid * cpt + j;
+        if (i < na) own += wsurv(i);
+    }
+    const unsigned long long exa = block_excl_scan(own, zsa, L.red.u);  // its barriers also publish bpre
+    const unsigned long long zs = zsa + zsb;
+    if (zs == 0ull) return true;
+    const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
+    MIS_STAMP(21);
+    if (tid == 0) L.uscratch[0] = ~0ull;
+    auto spec_below = [&](uint32_t x) -> unsigned long long {  // mass of the surviving specials with id < x
+        int lo = 0, hi = nbs;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (bids[mid] < x)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        return lo > 0 ? bpre[lo - 1] : 0ull;
+    };
+    __syncthreads();
+    // the tile candidates in token order, thread t walking [t c, (t + 1) c); its running sum left in place of the
+    // masses for the specials' search
+    if (own || nbs) {
+        unsigned long long c = exa;
+        for (int j = 0; j < cpt; ++j) {
+            const int i = tid * cpt + j;
+            if (i >= na) break;
+            const unsigned long long wi = wsurv(i);
+            c += wi;
+            if (wi) {
+                const uint32_t id = L.a.w.id[i] & ~kSelOnlyBit;
+                const unsigned long long cum = c + (nbs ? spec_below(id) : 0ull);
+                if (cum >= T2 && cum - wi < T2) L.uscratch[0] = id;
+            }
+            L.a.w.mass[i] = c;
+        }
+    }
+    MIS_STAMP(25);
+    __syncthreads();
+    MIS_STAMP(12);
+    if (tid < nbs) {
+        const uint32_t id = bids[tid];
+        int lo = 0, hi = na;  // tile candidates with id < this one
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if ((L.a.w.id[mid] & ~kSelOnlyBit) < id)
+                lo = mid + 1;
+            else
+                hi = mid;
+        }
+        const unsigned long long cum = (lo > 0 ? L.a.w.mass[lo - 1] : 0ull) + exb + wsorted;
+        if (cum >= T2 && cum - wsorted < T2) L.uscratch[0] = id;
+    }
+    __syncthreads();
+    MIS_STAMP(13);
+    if (L.uscratch[0] == ~0ull) return false;
+    out.token = (int64_t)L.uscratch[0];
+    return true;
+}
+
 // Top-p rows without top-k on bf16 logits whose nucleus the candidates do not hold.  The cut comes from every
 // slice's value counts and specials, as a weighted selection (one entry per value present with its count, one per
 // special; the tiny-magnitude lumps as one element at 0 with their summed mass, which may not be where the cut
@@ -2517,36 +3067,49 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
     const float u = tid == 0 ? row_uniform(G, R) : 0.f;
     if (w == 0) {  // lane s reads slice s's record
-        float mq = -INFINITY, mqd = -INFINITY;
-        int bad = 0, nsp = 0;
+        float mq = -INFINITY, mqd = -INFINITY, mr = -INFINITY, hb = -INFINITY;
+        double zz = 0.0;
+        int bad = 0, nsp = 0, nall = 0;
         unsigned long long tf = 0ull;
         if (l < S) {
             const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
             mq = pub_ld(&rec->mq);
             mqd = pub_ld(&rec->mqd);
+            mr = pub_ld(&rec->mref);
+            zz = pub_ld(&rec->z);
+            hb = pub_ld(&rec->gate);
             bad = (!pub_ld(&rec->hist) || (pub_ld(&rec->flags) & kRecOverflow)) ? 1 : 0;
-            nsp = pub_ld(&rec->nspec);
+            nall = pub_ld(&rec->nspec);
+            nsp = pub_ld(&rec->nhigh);
             tf = pub_ld(&rec->tinyfx);
         }
         const float m = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
         const float md = wave_reduce(mqd, [](float a, float b) { return fmaxf(a, b); });
+        const float hbm = wave_reduce(hb, [](float a, float b) { return fmaxf(a, b); });
         const int anybad = wave_reduce(bad, [](int a, int b) { return max(a, b); });
+        // the mass left out of the counts, relative to the row max, in the counts' fixed point
+        const double zr = wave_reduce((mr > -INFINITY && m > -INFINITY) ? zz * exp((double)mr - (double)m) : 0.0,
+                                      [](double a, double b) { return a + b; });
         const int incl = wave_incl_scan(nsp);
         if (l < S) {
             L.segoff[l] = incl - nsp;
             L.slice_u[l] = tf;
+            L.slice_n[l] = nall;
         }
         if (l == 0) {
             L.segoff[S] = __builtin_amdgcn_readlane(incl, 63);
             L.fscratch[0] = m;
             L.fscratch[1] = md;
+            L.fscratch[2] = hbm;
+            L.dscratch[0] = zr * kFx;
             L.token = anybad;
             L.nspec = 0;
         }
     }
     __syncthreads();
     if (L.token) return false;
-    const float m = L.fscratch[0], mdraw = L.fscratch[1];
+    const float m = L.fscratch[0], mdraw = L.fscratch[1], hbound = L.fscratch[2];
+    const double zrest = L.dscratch[0];
     const int ntot = L.segoff[S];
     out.thr = -INFINITY;
     out.mdraw = -INFINITY;
@@ -2659,7 +3222,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         const unsigned long long ex = block_excl_scan(wsum, tot, L.red.u);
         unsigned long long T = T0;
         if (frac > 0.0) {
-            const double pt = ceil(frac * (double)tot);
+            const double pt = ceil(frac * ((double)tot + zrest));
             T = pt < 1.0 ? 1ull : (unsigned long long)pt;
         }
         T_out = T;
@@ -2757,19 +3320,20 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     if (!scan_cut(0ull, (double)R.top_p, true, ck, codd, cbef, T)) return false;
     if (near_lump(ck)) return false;
     const float thr_p = codd ? resolve_odd(ck, T, cbef, true) : qt[ck];
-    if (!(thr_p == thr_p)) return false;
+    if (!(thr_p > hbound)) return false;  // the cut is not above every value the slices left out (or unresolved)
     float vmk = m;
     if (R.min_keep_eff >= 2) {
         if (scan_cut((unsigned long long)R.min_keep_eff, 0.0, false, ck, codd, cbef, Tk)) {
             if (near_lump(ck)) return false;
             vmk = codd ? resolve_odd(ck, (unsigned long long)R.min_keep_eff, cbef, false) : qt[ck];
-            if (!(vmk == vmk)) return false;
+            if (!(vmk > hbound)) return false;
         } else {
             vmk = -INFINITY;
         }
     }
     const float q_tlo = to_q<2>(R, -0.0078125f);
     const float thr = fminf(thr_p, vmk);
+    if (!(thr > hbound)) return false;
     const float md = mdraw >= thr ? mdraw : -INFINITY;
     out.thr = thr;
     out.mdraw = md;
@@ -2788,6 +3352,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     const bool lump_surv = nlump && thr <= q_tlo;
     if (tid < S) L.sbfx[tid] = lump_surv ? (unsigned long long)((double)L.slice_u[tid] * exp(-(double)md)) : 0ull;
     __syncthreads();
+    MIS_STAMP(16);
     // the counts: thread t weighs words t and t + kThreads of every slice's counts, the loads of four slices
     // issued together; one sum per wave and slice
     for (int s0 = 0; s0 < S; s0 += 4) {
@@ -2814,6 +3379,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
             if (l == 0 && acc) atomicAdd(&L.sbfx[s0 + u4], acc);
         }
     }
+    MIS_STAMP(17);
     // the specials, flattened over the slices (four loads per thread issued together); per wave, one sum for
     // each slice its entries span
     for (int i0 = 0; i0 < ntot; i0 += 4 * kThreads) {
@@ -2895,7 +3461,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     uint32_t* spid = (uint32_t*)(tsum + kThreads);            // the slice's specials: position and mass
     unsigned long long* spm = (unsigned long long*)(spid + kSpecCap);
     const unsigned long long* spl = (const unsigned long long*)(rec_base(G, R.row, ss) + kRecSpecOff);
-    const int nsp = min(L.segoff[ss + 1] - L.segoff[ss], kSpecCap);
+    const int nsp = min(L.slice_n[ss], kSpecCap);  // every special of the slice: their ids leave the pass
     unsigned long long se[2];
 #pragma unroll
     for (int u2 = 0; u2 < 2; ++u2) se[u2] = tid + u2 * kThreads < nsp ? pub_ld(spl + tid + u2 * kThreads) : 0ull;
@@ -2906,6 +3472,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     }
     tsum[tid] = 0ull;
     __syncthreads();
+    MIS_STAMP(19);
     const int eos = G.eos;
     if (tid == 0 && R.eos_rule != kEosNormal && eos >= slo && eos < shi) clear_keep_bit(L, g.first, eos);
     const int own_len = 8 * nc;
@@ -2924,6 +3491,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         }
     }
     __syncthreads();
+    MIS_STAMP(20);
     // survivor mass of the element at bf16 bits b whose keep bit is set
     auto elem_mass = [&](uint32_t b) -> unsigned long long {
         const int k = bf_key(b);
@@ -3168,6 +3736,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
     o.mdraw = -INFINITY;
     int path = MIS_PATH_FORCED;
     MIS_STAMP(7);
+
     if (!forced) {
         int mode = L.foreign ? kStream : R.mode;
         if (mode == kGreedy) {
@@ -3182,7 +3751,7 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
             MIS_STAMP(9);
         } else if (mode == kTopK || mode == kNucleus) {
             path = MIS_PATH_CANDIDATES;
-            if (!fin_cands(G, R, L, o)) mode = kStream;
+            if (!fin_sel(G, R, L, o)) mode = kStream;
             MIS_STAMP(8);
         }
         if (mode == kStream) {
