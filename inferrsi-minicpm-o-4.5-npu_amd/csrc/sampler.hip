@@ -102,6 +102,8 @@ struct DevGroup {
     const float* frequency;
     float t_val, p_val, rep_val, pres_val, freq_val;
     int32_t k_val;
+    int64_t zero64;   // 0: what a missing steps / finished array reads as
+    uint32_t one32;   // 1: what a missing active array reads as
     const float* alpha_lut;
     int32_t alpha_lut_len;
     int32_t hist_len;
@@ -275,17 +277,30 @@ struct RowIn {
     bool act, fin;
 };
 
+// Row parameters through the scalar cache: every address is selected without a branch (a missing array reads the
+// group's scalar value, which sits in the kernel arguments), so the loads issue back to back, ahead of the tile's,
+// and are waited for on their own counter.
+template <class T>
+__device__ __forceinline__ T sload(const T* p) {
+    return *(const __attribute__((address_space(4))) T*)p;
+}
+__device__ __forceinline__ bool sload_flag(const uint8_t* a, int row, const uint32_t* dflt) {
+    const uintptr_t addr = a ? (uintptr_t)(a + row) : (uintptr_t)dflt;
+    const uint32_t wd = sload((const uint32_t*)(addr & ~(uintptr_t)3));  // the aligned word holding the byte
+    return ((wd >> (8 * (uint32_t)(addr & 3))) & 0xffu) != 0u;
+}
+
 __device__ __forceinline__ RowIn load_row_in(const DevGroup& G, int row) {
     RowIn I;
-    I.step = G.steps ? gp(G.steps)[row] : 0;
-    I.t = G.temperature ? gp(G.temperature)[row] : G.t_val;
-    I.p = G.top_p ? gp(G.top_p)[row] : G.p_val;
-    I.rep = G.repetition ? gp(G.repetition)[row] : G.rep_val;
-    I.pres = G.presence ? gp(G.presence)[row] : G.pres_val;
-    I.freq = G.frequency ? gp(G.frequency)[row] : G.freq_val;
-    I.k = G.top_k ? gp(G.top_k)[row] : G.k_val;
-    I.act = G.active ? gp(G.active)[row] != 0 : true;
-    I.fin = G.finished ? gp(G.finished)[row] != 0 : false;
+    I.step = sload(G.steps ? G.steps + row : (const int64_t*)&G.zero64);
+    I.t = sload(G.temperature ? G.temperature + row : &G.t_val);
+    I.p = sload(G.top_p ? G.top_p + row : &G.p_val);
+    I.rep = sload(G.repetition ? G.repetition + row : &G.rep_val);
+    I.pres = sload(G.presence ? G.presence + row : &G.pres_val);
+    I.freq = sload(G.frequency ? G.frequency + row : &G.freq_val);
+    I.k = sload(G.top_k ? G.top_k + row : &G.k_val);
+    I.act = sload_flag(G.active, row, &G.one32);
+    I.fin = sload_flag(G.finished, row, (const uint32_t*)&G.zero64);
     return I;
 }
 
@@ -3990,6 +4005,8 @@ int mis_sample(const MisGroup* groups, int n_groups, void* workspace, size_t wor
         d.pres_val = g.presence_value;
         d.freq_val = g.frequency_value;
         d.k_val = g.top_k_value;
+        d.zero64 = 0;
+        d.one32 = 1u;
         d.alpha_lut = g.alpha_lut_len > 0 ? g.alpha_lut : nullptr;
         d.alpha_lut_len = g.alpha_lut ? g.alpha_lut_len : 0;
         d.hist_len = g.history ? g.history_len : 0;
