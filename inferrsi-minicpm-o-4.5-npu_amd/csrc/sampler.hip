@@ -2846,6 +2846,33 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
     }
     if (need_lo) qlo = -block_max4(make_float4(-vlo, -INFINITY, -INFINITY, -INFINITY), L.red).x;
     MIS_STAMP(27);
+    if (n <= 256) {
+        // a small set: wave 0 sorts it in registers, selects and draws (no workgroup barrier between the steps)
+        __syncthreads();
+        if (w == 0) {
+            const WSet ws = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
+            Outcome o;
+            bool ok;
+            if (n <= 64)
+                ok = wsort_select_draw<1>(R, ws, m_sel, zfull_fx, gate, ginf, u, o);
+            else if (n <= 128)
+                ok = wsort_select_draw<2>(R, ws, m_sel, zfull_fx, gate, ginf, u, o);
+            else
+                ok = wsort_select_draw<4>(R, ws, m_sel, zfull_fx, gate, ginf, u, o);
+            if (l == 0) {
+                L.token = ok ? 1 : 0;
+                L.fscratch[3] = o.thr;
+                L.dscratch[1] = o.mdraw;
+                L.uscratch[0] = (unsigned long long)o.token;
+            }
+        }
+        __syncthreads();
+        if (!L.token) return false;
+        out.thr = L.fscratch[3];
+        out.mdraw = (float)L.dscratch[1];
+        out.token = (int64_t)L.uscratch[0];
+        return true;
+    }
     SelBins B;
     B.qmin = qlo;
     B.scale = qhi > qlo ? fminf((float)kSelBins / (qhi - qlo), 1e30f) : 0.0f;

@@ -372,6 +372,35 @@ def test_graph_replay_equals_eager():
         assert torch.equal(grp.tokens, eager)
 
 
+def test_graph_replay_after_the_stream_workspace_is_outgrown():
+    """A graph captured on a stream keeps its workspace: a later, larger launch on that stream takes a new one and the
+    graph's replays still match the eager tokens (the outgrown buffer stays alive for the graph)."""
+    print("[gpu] graph replay after workspace growth", flush=True)
+    small = W.talker_b8("hf").to(DEV)
+    big = W.thinker_b64().to(DEV)
+    eager_small = G.sample(small.logits, **small.group_kwargs()).tokens.clone()
+    eager_big = G.sample(big.logits, **big.group_kwargs()).tokens.clone()
+    torch.cuda.synchronize()
+    grp = G.RowGroup(small.logits, **small.group_kwargs())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        G.launch([grp])  # the stream's workspace, sized for the small launch
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            G.launch([grp])
+        torch.cuda.synchronize()
+        for _ in range(3):
+            gb = G.RowGroup(big.logits, **big.group_kwargs())
+            G.launch([gb])  # outgrows the stream's workspace
+            grp.tokens.fill_(-7)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(gb.tokens, eager_big)
+            assert torch.equal(grp.tokens, eager_small)
+
+
 def test_errors_are_loud():
     with pytest.raises(ValueError):
         G.RowGroup(torch.zeros(2, 8))  # CPU tensor: no CPU path
