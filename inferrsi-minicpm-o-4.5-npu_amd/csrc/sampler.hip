@@ -269,6 +269,12 @@ struct Row {
     bool hf, greedy, filters, p_active, pen, live, want_out, needz;
 };
 
+struct Outcome {
+    int64_t token;
+    float thr;    // survivors: q >= thr (and drawable)
+    float mdraw;  // reference of the survivors' masses
+};
+
 // The row's parameters as loaded (a slice issues these loads before its tile's: loads return in order).
 struct RowIn {
     int64_t step;
@@ -808,7 +814,230 @@ __device__ __forceinline__ bool nucleus_hist(const Row& R, int es) {
     return es == 2 && R.mode == kNucleus && R.T >= kHistMinT;
 }
 
-enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2 };
+// ------------------------------------------------------------------ the histogram path's second round
+//
+// After a top-p row's cut is settled from the value counts, the draw needs the survivor mass of every 512-value
+// sub-block of the row.  The row's slices other than the finaliser keep their tiles in registers and wait on the
+// row's line.  The finaliser first publishes the draw's reference md (the row's largest drawable value), and the
+// waiting slices build the table of masses by value (r2_lut) while it settles the cut; then it publishes the
+// decision, each slice sums its sub-blocks and counts itself in a second time, and the last to do so draws inside
+// the one sub-block that holds the target.  A waiting slice waits only for its row's finaliser, which has arrived
+// and is running, so the wait ends whatever the scheduling; a slice that still gives up (after kR2SpinTicks) counts
+// itself in with a failure mark, and the row then comes out as PAD, with the workspace's error word raised, and its
+// state untouched.
+
+constexpr int kLineDec = 64;  // u32 on the row's line: 0 pending, 3 md published, 1 settled by the finaliser (the
+                              // row is streamed), 2 sub-block sums wanted
+constexpr int kLineR2 = 68;   // u32: second-round arrivals (low 16 bits) and failures (high 16 bits)
+constexpr int kLineDat = 72;  // f32 thr, md, x0 (the least bf16 value x with x / T >= thr), u (the row's uniform)
+constexpr unsigned long long kR2SpinTicks = 200000ull;  // 2 ms of the 100 MHz real-time counter
+static_assert(kLineDat + 16 <= kLineBytes, "row line");
+// The mass table (kKeys + 1 entries of 8 bytes) lies in L.a past what the histogram finaliser keeps there (its
+// per-key tables, below 64 KB) and past a slice's counts, so a slice can build it before the cut is known.
+constexpr int kLutOff = 65536;
+static_assert(kLutOff + 8 * (kKeys + 1) <= (int)sizeof(Lds::a), "mass table");
+static_assert(16 * (kKeys + 1) + 12 * 256 <= kLutOff, "the histogram finaliser's tables");
+
+__device__ __forceinline__ char* row_line(const KernelArgs& A, const Row& R) {
+    return A.arrive + (int64_t)R.grow * kLineBytes;
+}
+
+// The finaliser's words to the waiting slices (thread 0): dec 3 with md, then 1, or 2 with thr, md, x0, u.
+__device__ __forceinline__ void r2_decide(const KernelArgs& A, const Row& R, unsigned dec, float thr, float md, float x0,
+                                          float u) {
+    if (threadIdx.x != 0) return;
+    char* line = row_line(A, R);
+    float* d = (float*)(line + kLineDat);
+    if (dec == 2u) {
+        d[0] = thr;
+        d[2] = x0;
+        d[3] = u;
+    }
+    if (dec != 1u) {
+        d[1] = md;
+        wait_stores();
+    }
+    __hip_atomic_store((unsigned*)(line + kLineDec), dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int lut_key(uint32_t b) {  // the exact key of bf16 pattern b, or kKeys for a lump
+    const uint32_t a = b & 0x7fffu;
+    const uint32_t m = a - kBfLo;
+    const int k = (b & 0x8000u) ? kKeyZero - 2 - (int)m : kKeyZero + 2 + (int)m;
+    return a == 0u ? kKeyZero : (m < kBfHi - kBfLo ? k : kKeys);
+}
+
+__device__ __forceinline__ unsigned long long* lut_of(Lds& L) {
+    return (unsigned long long*)((char*)&L.a + kLutOff);
+}
+
+// The masses by value (every thread): lut[k] = efx(x / T, md) for every exact histogram key k with x / T <= md
+// (x its bf16 value), 0 for the others and at lut[kKeys], which every lump maps to: a lump's values differ from one
+// another, so they are weighed one by one.
+__device__ __forceinline__ void r2_lut(const Row& R, Lds& L, float md) {
+    unsigned long long* lut = lut_of(L);
+    for (int k = threadIdx.x; k <= kKeys; k += kThreads) {
+        unsigned long long v = 0ull;
+        if (key_exact(k)) {
+            const float q = to_q<2>(R, key_bf(k));
+            if (q <= md) v = efx(q, md);
+        }
+        lut[k] = v;
+    }
+}
+
+// A waiting slice: the decision (0 if it gave up waiting), with thr, md, x0, u in L.fscratch when it is 2; the mass
+// table is built on the way, as soon as md is out.
+__device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, Lds& L) {
+    char* line = row_line(A, R);
+    unsigned* dw = (unsigned*)(line + kLineDec);
+    const float* dat = (const float*)(line + kLineDat);
+    const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+    bool have_lut = false;
+    for (;;) {
+        if (threadIdx.x == 0) {
+            unsigned d = __hip_atomic_load(dw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            while (d == 0u || (have_lut && d == 3u)) {
+                if (__builtin_amdgcn_s_memrealtime() - t0 > kR2SpinTicks) {
+                    d = 0u;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+                d = __hip_atomic_load(dw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (d == 2u) {
+                L.fscratch[0] = pub_ld(dat);
+                L.fscratch[2] = pub_ld(dat + 2);
+                L.fscratch[3] = pub_ld(dat + 3);
+            }
+            if (d >= 2u) L.fscratch[1] = pub_ld(dat + 1);
+            L.token = (int)d;
+        }
+        __syncthreads();
+        const unsigned d = (unsigned)L.token;
+        if (d == 0u || d == 1u) return d;
+        if (!have_lut) {
+            r2_lut(R, L, L.fscratch[1]);
+            have_lut = true;
+        }
+        __syncthreads();  // the table complete, and L.token read by every thread before thread 0 writes it again
+        if (d == 2u) return d;
+    }
+}
+
+// Second-round arrival (every thread): true in the row's last workgroup, which also gets the decision as it stood
+// and whether some slice gave up; the last one leaves the row's words zero for the next launch.
+__device__ __forceinline__ bool r2_arrive(const KernelArgs& A, const Row& R, Lds& L, bool gave_up, unsigned& dec,
+                                          bool& failed) {
+    wait_stores();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        char* line = row_line(A, R);
+        unsigned* w2 = (unsigned*)(line + kLineR2);
+        unsigned* dw = (unsigned*)(line + kLineDec);
+        const unsigned add = 1u + (gave_up ? 0x10000u : 0u);
+        const unsigned now = __hip_atomic_fetch_add(w2, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+        const int last = (int)(now & 0xffffu) == R.S;
+        unsigned d = 0u;
+        if (last) {
+            d = __hip_atomic_load(dw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(dw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(w2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        L.is_last = last;
+        L.foreign = (now >> 16) != 0u ? 1 : 0;
+        L.flags = (int)d;
+    }
+    __syncthreads();
+    dec = (unsigned)L.flags;
+    failed = L.foreign != 0;
+    return L.is_last != 0;
+}
+
+// The mass of one surviving tile element (bf16 pattern b): the table's, or 0 with its bit in `lumps` when b is a
+// lump value, which the caller weighs with efx.
+__device__ __forceinline__ unsigned long long r2_mass(const unsigned long long* lut, uint32_t b, int e,
+                                                      uint32_t& lumps) {
+    const int k = lut_key(b);
+    if (k == kKeys) lumps |= 1u << e;
+    return lut[k];
+}
+
+// The survivor mass of every (wave, round) sub-block of a bf16 tile (masked values -inf) and of the slice's
+// specials in L.spec (ns of them), published to the slice's record.  Survivors: x >= x0 (q = x / T >= thr), and the
+// drawable specials with q >= thr.  The mass table must be built.
+__device__ __forceinline__ void r2_sums(const DevGroup& G, const Row& R, Lds& L, const uint4 (&t)[kRounds], int RR,
+                                        int first, int ns, float thr, float md, float x0) {
+    const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+    const unsigned long long* lut = lut_of(L);
+    if (tid < kMaxSB) L.sbfx[tid] = 0ull;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+        if (r >= RR) continue;
+        // the survivors as a mask first: the table is read for them alone
+        uint32_t bits = 0u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) bits |= tile_val<2>(t[r], e) >= x0 ? (1u << e) : 0u;
+        unsigned long long acc = 0ull;
+        if (ballot(bits != 0u)) {
+            uint32_t lumps = 0u;
+            while (bits) {
+                const int e = __ffs(bits) - 1;
+                bits &= bits - 1u;
+                acc += r2_mass(lut, __float_as_uint(tile_val_dyn<2>(t[r], e)) >> 16, e, lumps);
+            }
+            if (ballot(lumps != 0u)) {  // rare: values within 2^-7 of zero
+                while (lumps) {
+                    const int e = __ffs(lumps) - 1;
+                    lumps &= lumps - 1u;
+                    acc += efx(to_q<2>(R, tile_val_dyn<2>(t[r], e)), md);
+                }
+            }
+            acc = wave_reduce(acc, [](unsigned long long a, unsigned long long b) { return a + b; });
+        }
+        if (l == 0) L.sbfx[w * RR + r] = acc;
+    }
+    __syncthreads();
+    MIS_STAMP(17);
+    for (int i = tid; i < ns; i += kThreads) {
+        const Special sp = L.spec[i];
+        if (!sp.sel && sp.q >= thr) atomicAdd(&L.sbfx[(sp.j - first) >> 9], efx(sp.q, md));
+    }
+    __syncthreads();
+    MIS_STAMP(18);
+    unsigned long long* sb = (unsigned long long*)(rec_base(G, R.row, R.slice) + kRecSbOff);
+    if (tid < kWaves * RR) sb[tid] = L.sbfx[tid];
+}
+
+// The least bf16 value x with x / T >= thr (finite thr), the same in every lane of the calling wave: x0 lies within
+// a few bf16 steps of thr T, so the 64 values around it are tried at once; a binary search over the order of bf16
+// bit patterns settles the rest.
+__device__ __forceinline__ float r2_x0(const Row& R, float thr) {
+    auto val = [](uint32_t o) {  // bf16 value of order index o (0x007f: -inf ... 0xff80: +inf)
+        const uint32_t b = (o & 0x8000u) ? (o & 0x7fffu) : (~o & 0xffffu);
+        return __uint_as_float(b << 16);
+    };
+    const uint32_t yb = __float_as_uint(thr * R.T) >> 16;
+    const int oc = (int)((yb & 0x8000u) ? (~yb & 0xffffu) : (yb | 0x8000u));
+    const int o = min(max(oc - 32 + lane_id(), 0x0080), 0xff80);
+    const uint64_t hit = ballot(to_q<2>(R, val((uint32_t)o)) >= thr);
+    if (hit && !(hit & 1ull)) return val((uint32_t)min(max(oc - 32 + __ffsll((long long)hit) - 1, 0x0080), 0xff80));
+    uint32_t lo = 0x007fu, hi = 0xff80u;  // to_q(val(lo)) < thr <= to_q(val(hi))
+    while (hi - lo > 1u) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (to_q<2>(R, val(mid)) >= thr)
+            hi = mid;
+        else
+            lo = mid;
+    }
+    return val(hi);
+}
+
+__device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
+                                        Outcome& out, float& u);
+
+enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2, kActR2Draw = 3, kActR2Failed = 4, kActStream = 5 };
 
 // One slice workgroup: loads, the row's pipeline on the tile, publication, arrival.  Returns kActFinalize in the
 // row's last workgroup to arrive (R then holds the row), kActForced in slice 0 of a row whose EOS is forced.
@@ -1140,7 +1369,41 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 rec->nhigh = L.nhi;
                 rec->tinyfx = L.tinyfx;
             }
-            return arrive(A, R, L) ? kActFinalize : kActNone;
+            unsigned dec;
+            bool failed;
+            if (!arrive(A, R, L)) {
+                // held for the second round, the tile still in registers
+                const unsigned d = r2_wait(A, R, L);
+                MIS_STAMP(9);
+                if (d == 2u) r2_sums(G, R, L, t, RR, geo.first, ns, L.fscratch[0], L.fscratch[1], L.fscratch[2]);
+                MIS_STAMP(15);
+                if (r2_arrive(A, R, L, d == 0u, dec, failed) && dec == 2u) return failed ? kActR2Failed : kActR2Draw;
+                return kActNone;
+            }
+            // the row's finaliser, its tile still in registers: the cut from every slice's counts, then its own
+            // sub-block sums like the others'
+            Outcome o;
+            float u = 0.f;
+            const int res = L.foreign ? 0 : fin_hist(A, G, R, L, o, u);
+            MIS_STAMP(9);
+            if (res != 2) {  // the row is streamed (or has no survivor): the waiting slices are released
+                r2_decide(A, R, 1u, 0.f, 0.f, 0.f, 0.f);
+                (void)r2_arrive(A, R, L, false, dec, failed);
+                return kActStream;
+            }
+            const float x0 = r2_x0(R, o.thr);
+            r2_decide(A, R, 2u, o.thr, o.mdraw, x0, u);
+            if (tid == 0) {  // for r2_finish, as a waiting slice has them
+                L.fscratch[0] = o.thr;
+                L.fscratch[1] = o.mdraw;
+                L.fscratch[2] = x0;
+                L.fscratch[3] = u;
+            }
+            MIS_STAMP(14);
+            r2_sums(G, R, L, t, RR, geo.first, ns, o.thr, o.mdraw, x0);
+            MIS_STAMP(15);
+            if (r2_arrive(A, R, L, false, dec, failed) && dec == 2u) return failed ? kActR2Failed : kActR2Draw;
+            return kActNone;
         }
     }
 
@@ -1454,11 +1717,6 @@ __device__ __forceinline__ bool range_find(Visit& V, int sel, bool desc, unsigne
     return true;
 }
 
-struct Outcome {
-    int64_t token;
-    float thr;    // survivors: q >= thr (and drawable)
-    float mdraw;  // reference of the survivors' masses
-};
 
 // The top-k / top-p selection (engine/talker_sampler.py:95-133) and the draw (:161-172) over a visited set.
 // m_sel: max over everything ranked; zfull_fx: the whole-vocabulary normaliser in fixed point relative to m_sel
@@ -2036,14 +2294,19 @@ __device__ __forceinline__ void wave_bitonic(unsigned long long (&v)[P]) {
 }
 
 // The value of x[] at rank r (uniform r < 64 P): element r of the rank order.
+// Each element is read out of its lane first and the pick is made among the scalar results, so no per-lane value is
+// ever indexed by r.
 template <int P, class T>
 __device__ __forceinline__ T at_rank(const T (&x)[P], int r) {
-    T y = x[0];
+    T y = (T)0;
 #pragma unroll
-    for (int p = 1; p < P; ++p)
-        if ((r >> 6) == p) y = x[p];
-    if constexpr (sizeof(T) == 8) return (T)readlane_u64((unsigned long long)y, r & 63);
-    else return (T)__builtin_amdgcn_readlane((int)y, r & 63);
+    for (int p = 0; p < P; ++p) {
+        T z;
+        if constexpr (sizeof(T) == 8) z = (T)readlane_u64((unsigned long long)x[p], r & 63);
+        else z = (T)__builtin_amdgcn_readlane((int)x[p], r & 63);
+        if ((r >> 6) == p) y = z;
+    }
+    return y;
 }
 
 // select_draw for at most 64 P candidates (n >= 1), on wave 0.
@@ -3105,9 +3368,11 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
 // special; the tiny-magnitude lumps as one element at 0 with their summed mass, which may not be where the cut
 // falls).  Each slice's survivor mass follows from its counts; the draw streams the one slice that holds it.
 // False: the row is streamed instead.
-__device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
+// 0: the row must be streamed; 1: no survivor; 2: the cut (out.thr, out.mdraw) for the second round.
+__device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L, Outcome& out,
+                                        float& u) {
     const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
-    const float u = tid == 0 ? row_uniform(G, R) : 0.f;
+    if (tid == 0) L.fscratch[3] = row_uniform(G, R);  // the draw's, for the second round
     if (w == 0) {  // lane s reads slice s's record
         float mq = -INFINITY, mqd = -INFINITY, mr = -INFINITY, hb = -INFINITY;
         double zz = 0.0;
@@ -3149,20 +3414,41 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         }
     }
     __syncthreads();
-    if (L.token) return false;
+    if (L.token) return 0;
     const float m = L.fscratch[0], mdraw = L.fscratch[1], hbound = L.fscratch[2];
     const double zrest = L.dscratch[0];
     const int ntot = L.segoff[S];
     out.thr = -INFINITY;
     out.mdraw = -INFINITY;
     out.token = R.V - 1;
-    if (!(m > -INFINITY)) return true;
-    // every slice's counts, merged (the loads of four slices issued together)
+    if (!(m > -INFINITY)) return 1;
+    u = L.fscratch[3];
+    // md to the waiting slices, which build their mass tables while the cut is settled here
+    if (mdraw > -INFINITY) r2_decide(A, R, 3u, 0.f, mdraw, 0.f, 0.f);
+    // every slice's counts, merged: the first four slices' loads are in flight while the mass table is built
     uint32_t* cnt = (uint32_t*)L.h.w;
-    for (int i0 = 0; i0 < kHistWords; i0 += kThreads) {
-        const int i = i0 + tid;
+    constexpr int kMI = (kHistWords + kThreads - 1) / kThreads;
+    uint32_t hv[kMI][4];
+#pragma unroll
+    for (int mi = 0; mi < kMI; ++mi) {
+        const int i = mi * kThreads + tid;
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4)
+            hv[mi][u4] = (i < kHistWords && u4 < S)
+                             ? pub_ld((const uint32_t*)(rec_base(G, R.row, u4) + kRecHistOff) + i)
+                             : 0u;
+    }
+    if (mdraw > -INFINITY) r2_lut(R, L, mdraw);
+#pragma unroll
+    for (int mi = 0; mi < kMI; ++mi) {
+        const int i = mi * kThreads + tid;
         uint32_t a = 0u, b = 0u;
-        for (int s0 = 0; s0 < S; s0 += 4) {
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4) {
+            a += hv[mi][u4] & 0xffffu;
+            b += hv[mi][u4] >> 16;
+        }
+        for (int s0 = 4; s0 < S; s0 += 4) {
             uint32_t v[4];
 #pragma unroll
             for (int u4 = 0; u4 < 4; ++u4)
@@ -3194,7 +3480,7 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     }
     __syncthreads();
     const uint32_t nlump = cnt[kKeyZero - 1] + cnt[kKeyZero + 1];
-    if (cnt[kKeys - 1] != 0u) return false;  // values of 256 and above are not resolved here
+    if (cnt[kKeys - 1] != 0u) return 0;  // values of 256 and above are not resolved here
     // every special into the bin its slice found for it: the even bin of the exact key holding its value (counted
     // with that key), or the odd bin strictly between that key and the next exact one
     auto spec_at = [&](int i, unsigned long long& e, int& bin) {
@@ -3296,10 +3582,10 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
         const int b = L.token;
         before_out = L.uscratch[1];
         __syncthreads();
-        if (b < 0) return false;
+        if (b < 0) return 0;
         key_out = b >> 1;
         odd_out = (b & 1) != 0;
-        return true;
+        return 1;
     };
     // the value at which the cumulative weight reaches T inside odd bin k: its specials sorted by value
     // (descending), walked from `before`; NaN when it cannot be resolved here
@@ -3359,254 +3645,27 @@ __device__ __forceinline__ bool fin_hist(const DevGroup& G, const Row& R, Lds& L
     bool codd;
     unsigned long long cbef, T, Tk;
     MIS_STAMP(12);
-    if (!scan_cut(0ull, (double)R.top_p, true, ck, codd, cbef, T)) return false;
-    if (near_lump(ck)) return false;
+    if (!scan_cut(0ull, (double)R.top_p, true, ck, codd, cbef, T)) return 0;
+    if (near_lump(ck)) return 0;
     const float thr_p = codd ? resolve_odd(ck, T, cbef, true) : qt[ck];
-    if (!(thr_p > hbound)) return false;  // the cut is not above every value the slices left out (or unresolved)
+    if (!(thr_p > hbound)) return 0;  // the cut is not above every value the slices left out (or unresolved)
     float vmk = m;
     if (R.min_keep_eff >= 2) {
         if (scan_cut((unsigned long long)R.min_keep_eff, 0.0, false, ck, codd, cbef, Tk)) {
-            if (near_lump(ck)) return false;
+            if (near_lump(ck)) return 0;
             vmk = codd ? resolve_odd(ck, (unsigned long long)R.min_keep_eff, cbef, false) : qt[ck];
-            if (!(vmk > hbound)) return false;
+            if (!(vmk > hbound)) return 0;
         } else {
             vmk = -INFINITY;
         }
     }
     const float q_tlo = to_q<2>(R, -0.0078125f);
     const float thr = fminf(thr_p, vmk);
-    if (!(thr > hbound)) return false;
+    if (!(thr > hbound)) return 0;
     const float md = mdraw >= thr ? mdraw : -INFINITY;
     out.thr = thr;
     out.mdraw = md;
-    if (!(md > -INFINITY)) return true;
-    // survivor masses by key (relative to md), then per slice: counts, specials, the lumps when they survive
-    unsigned long long* lut = (unsigned long long*)L.a.c.q;
-    for (int k = tid; k <= kKeys; k += kThreads) {
-        unsigned long long e = 0ull;
-        if (k < kKeys && key_exact(k)) {
-            const float q = to_q<2>(R, key_bf(k));
-            if (q >= thr) e = efx(q, md);
-        }
-        lut[k] = e;
-    }
-    MIS_STAMP(13);
-    const bool lump_surv = nlump && thr <= q_tlo;
-    if (tid < S) L.sbfx[tid] = lump_surv ? (unsigned long long)((double)L.slice_u[tid] * exp(-(double)md)) : 0ull;
-    __syncthreads();
-    MIS_STAMP(16);
-    // the counts: thread t weighs words t and t + kThreads of every slice's counts, the loads of four slices
-    // issued together; one sum per wave and slice
-    for (int s0 = 0; s0 < S; s0 += 4) {
-        uint32_t v[4][2];
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            const uint32_t* hg = (const uint32_t*)(rec_base(G, R.row, min(s0 + u4, S - 1)) + kRecHistOff);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int i = tid + h * kThreads;
-                v[u4][h] = (s0 + u4 < S && i < kHistWords) ? pub_ld(hg + i) : 0u;
-            }
-        }
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            unsigned long long acc = 0ull;
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int i = min(tid + h * kThreads, kHistWords - 1);
-                acc += (unsigned long long)(v[u4][h] & 0xffffu) * lut[2 * i] +
-                       (unsigned long long)(v[u4][h] >> 16) * lut[2 * i + 1];
-            }
-            acc = wave_sum(acc);
-            if (l == 0 && acc) atomicAdd(&L.sbfx[s0 + u4], acc);
-        }
-    }
-    MIS_STAMP(17);
-    // the specials, flattened over the slices (four loads per thread issued together); per wave, one sum for
-    // each slice its entries span
-    for (int i0 = 0; i0 < ntot; i0 += 4 * kThreads) {
-        unsigned long long e[4];
-        int sl[4];
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            const int i = i0 + u4 * kThreads + tid;
-            int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (L.segoff[mid] <= i)
-                    lo = mid;
-                else
-                    hi = mid;
-            }
-            sl[u4] = i < ntot ? lo : -1;
-            e[u4] = i < ntot ? pub_ld((const unsigned long long*)(rec_base(G, R.row, lo) + kRecSpecOff) +
-                                      (i - L.segoff[lo]))
-                             : 0ull;
-        }
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            const float q = __uint_as_float((uint32_t)e[u4]);
-            const unsigned long long m2 =
-                (sl[u4] >= 0 && !((uint32_t)(e[u4] >> 32) & kSelOnlyBit) && q >= thr) ? efx(q, md) : 0ull;
-            const int smin = wave_reduce(sl[u4] >= 0 ? sl[u4] : S, [](int a, int b) { return min(a, b); });
-            const int smax = wave_reduce(sl[u4], [](int a, int b) { return max(a, b); });
-            for (int sx = smin; sx <= smax; ++sx) {
-                const unsigned long long a = wave_sum(sl[u4] == sx ? m2 : 0ull);
-                if (l == 0 && a) atomicAdd(&L.sbfx[sx], a);
-            }
-        }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        unsigned long long zs = 0ull;
-        for (int s = 0; s < S; ++s) zs += L.sbfx[s];
-        int ss = -1;
-        unsigned long long rem = 0ull;
-        if (zs > 0ull) {
-            const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
-            unsigned long long c = 0ull;
-            for (int s = 0; s < S; ++s) {
-                const unsigned long long v = L.sbfx[s];
-                if (v && c + v >= T2) {
-                    ss = s;
-                    rem = T2 - c;
-                    break;
-                }
-                c += v;
-            }
-        }
-        L.is_last = ss;
-        L.uscratch[0] = rem;
-    }
-    __syncthreads();
-    const int ss = L.is_last;
-    const unsigned long long rem = L.uscratch[0];
-    MIS_STAMP(14);
-    if (ss < 0) return true;
-    // the draw inside slice ss in one pass over it: thread t owns chunks [t nc, (t + 1) nc) (8 elements each, from
-    // the slice's 16-byte aligned start) and sums their survivor masses (the specials from their list, added to
-    // their owner); one scan finds the owner of the target, whose wave walks its elements in token order
-    const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
-    const Geo<2> g = slice_geo<2>(G, R.row, slo);
-    const int nch = (shi - g.first + 7) / 8;
-    const int nc = (nch + kThreads - 1) / kThreads;  // <= kRounds
-    const int jb = (g.first >> 5) << 5;
-    const int nkw = min(kKeepWords, (shi - jb + 31) / 32);
-    uint32_t mwv[2];
-#pragma unroll
-    for (int u2 = 0; u2 < 2; ++u2) mwv[u2] = mask_word(G, R.row, jb, tid + u2 * kThreads, nkw);
-    uint4 cv[kRounds];
-#pragma unroll
-    for (int c = 0; c < kRounds; ++c)
-        cv[c] = c < nc ? load_chunk<2>(g, tid * nc + c, shi) : make_uint4(0u, 0u, 0u, 0u);
-    unsigned long long* tsum = (unsigned long long*)L.a.c.id;  // per thread
-    uint32_t* spid = (uint32_t*)(tsum + kThreads);            // the slice's specials: position and mass
-    unsigned long long* spm = (unsigned long long*)(spid + kSpecCap);
-    const unsigned long long* spl = (const unsigned long long*)(rec_base(G, R.row, ss) + kRecSpecOff);
-    const int nsp = min(L.slice_n[ss], kSpecCap);  // every special of the slice: their ids leave the pass
-    unsigned long long se[2];
-#pragma unroll
-    for (int u2 = 0; u2 < 2; ++u2) se[u2] = tid + u2 * kThreads < nsp ? pub_ld(spl + tid + u2 * kThreads) : 0ull;
-#pragma unroll
-    for (int u2 = 0; u2 < 2; ++u2) {
-        const int k = tid + u2 * kThreads;
-        if (k < kKeepWords) L.keep[k] = k < nkw ? mwv[u2] & range_bits(jb + 32 * k, slo, shi) : 0u;
-    }
-    tsum[tid] = 0ull;
-    __syncthreads();
-    MIS_STAMP(19);
-    const int eos = G.eos;
-    if (tid == 0 && R.eos_rule != kEosNormal && eos >= slo && eos < shi) clear_keep_bit(L, g.first, eos);
-    const int own_len = 8 * nc;
-#pragma unroll
-    for (int u2 = 0; u2 < 2; ++u2) {
-        const int i = tid + u2 * kThreads;
-        if (i < nsp) {
-            const unsigned long long e = se[u2];
-            const int j = (int)((uint32_t)(e >> 32) & ~kSelOnlyBit);
-            const float q = __uint_as_float((uint32_t)e);
-            const unsigned long long m2 = (!((uint32_t)(e >> 32) & kSelOnlyBit) && q >= thr) ? efx(q, md) : 0ull;
-            clear_keep_bit(L, g.first, j);
-            spid[i] = (uint32_t)(j - g.first);
-            spm[i] = m2;
-            if (m2) atomicAdd(&tsum[(j - g.first) / own_len], m2);
-        }
-    }
-    __syncthreads();
-    MIS_STAMP(20);
-    // survivor mass of the element at bf16 bits b whose keep bit is set
-    auto elem_mass = [&](uint32_t b) -> unsigned long long {
-        const int k = bf_key(b);
-        if (lump_surv && (k == kKeyZero - 1 || k == kKeyZero + 1)) return efx(to_q<2>(R, __uint_as_float(b << 16)), md);
-        return lut[k];
-    };
-    unsigned long long acc = 0ull;
-#pragma unroll
-    for (int c = 0; c < kRounds; ++c) {
-        if (c >= nc) continue;
-        const uint32_t kb = chunk_keep<2>(L, g.first, tid * nc + c);
-        const uint32_t wv[4] = {cv[c].x, cv[c].y, cv[c].z, cv[c].w};
-        if (lump_surv) {
-#pragma unroll
-            for (int h = 0; h < 8; ++h)
-                if ((kb >> h) & 1u) acc += elem_mass((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu);
-        } else {
-            // every key's mass read before any is added (independent LDS reads in flight together)
-            unsigned long long mv[8];
-#pragma unroll
-            for (int h = 0; h < 8; ++h) mv[h] = lut[bf_key((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu)];
-#pragma unroll
-            for (int h = 0; h < 8; ++h) acc += ((kb >> h) & 1u) ? mv[h] : 0ull;
-        }
-    }
-    MIS_STAMP(24);
-    const unsigned long long mine = tsum[tid] + acc;
-    unsigned long long tot;
-    const unsigned long long ex = block_excl_scan(mine, tot, L.red.u);
-    if (tid == 0) L.token = -1;
-    __syncthreads();
-    MIS_STAMP(25);
-    if (mine && ex < rem && rem <= ex + mine) {
-        L.token = tid;
-        L.uscratch[1] = rem - ex;
-    }
-    __syncthreads();
-    const int own = L.token;
-    if (own < 0) return false;  // the slice holds less than its share (the lumps' summed masses round differently)
-    // the owner's chunks and keep bits to LDS; its specials' masses by position
-    uint4* ochunk = (uint4*)L.gh;
-    unsigned long long* om = L.sbfx;  // own_len <= 8 kRounds entries
-    if (tid == own) {
-#pragma unroll
-        for (int c = 0; c < kRounds; ++c)
-            if (c < nc) ochunk[c] = cv[c];
-    }
-    if (tid < own_len) om[tid] = 0ull;
-    __syncthreads();
-    for (int i = tid; i < nsp; i += kThreads) {
-        const int pos = (int)spid[i] - own * own_len;
-        if (pos >= 0 && pos < own_len) om[pos] = spm[i];
-    }
-    __syncthreads();
-    if (wave_id() == 0) {
-        const int i = lane_id();
-        unsigned long long wm = 0ull;
-        if (i < own_len) {
-            const int c = i >> 3, h = i & 7;
-            const uint4 v = ochunk[min(c, kRounds - 1)];
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-            const uint32_t kb = chunk_keep<2>(L, g.first, own * nc + c);
-            wm = ((kb >> h) & 1u) ? elem_mass((wv[h >> 1] >> (16 * (h & 1))) & 0xffffu) : om[i];
-        }
-        const unsigned long long incl = wave_incl_scan(wm);
-        const uint64_t hit = ballot(wm && incl >= L.uscratch[1]);
-        if (lane_id() == 0)
-            L.uscratch[0] = hit ? (unsigned long long)(g.first + own * own_len + __ffsll((long long)hit) - 1) : ~0ull;
-    }
-    __syncthreads();
-    if (L.uscratch[0] == ~0ull) return false;
-    out.token = (int64_t)L.uscratch[0];
-    return true;
+    return md > -INFINITY ? 2 : 1;
 }
 
 __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
@@ -3770,6 +3829,180 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Row& R, in
     }
 }
 
+// The draw (engine/talker_sampler.py:161-172) from every slice's sub-block sums and the row's uniform u: the
+// sub-block that holds the target, then its 512 values in token order on one wave, weighed with the mass table.
+// Returns the token.
+__device__ __forceinline__ int64_t r2_draw(const DevGroup& G, const Row& R, Lds& L, float thr, float md, float x0,
+                                           float u) {
+    const int tid = threadIdx.x, l = lane_id();
+    const int nsb = kWaves * G.R, total = R.S * nsb;
+    const int per = (total + kThreads - 1) / kThreads;  // thread t: sums [t per, (t + 1) per) in (slice, sub-block) order
+    unsigned long long v[kMaxSlices * kMaxSB / kThreads + 1];
+    unsigned long long own = 0ull;
+#pragma unroll
+    for (int k = 0; k < kMaxSlices * kMaxSB / kThreads + 1; ++k) {
+        const int i = tid * per + k;
+        v[k] = 0ull;
+        if (k < per && i < total)
+            v[k] = pub_ld((const unsigned long long*)(rec_base(G, R.row, i / nsb) + kRecSbOff) + (i % nsb));
+        own += v[k];
+    }
+    unsigned long long zs;
+    if (tid == 0) L.token = -1;
+    const unsigned long long ex = block_excl_scan(own, zs, L.red.u);
+    const unsigned long long T2 = zs ? (unsigned long long)floor((double)u * (double)zs) + 1ull : 0ull;
+    if (own && ex < T2 && T2 <= ex + own) {
+        unsigned long long c = ex;
+#pragma unroll
+        for (int k = 0; k < kMaxSlices * kMaxSB / kThreads + 1; ++k) {
+            if (k >= per) break;
+            if (v[k] && c + v[k] >= T2) {
+                L.token = tid * per + k;
+                L.uscratch[1] = T2 - c;
+                break;
+            }
+            c += v[k];
+        }
+    }
+    __syncthreads();
+    const int hit = L.token;
+    MIS_STAMP(19);
+    if (hit < 0) return R.V - 1;  // no survivor mass (cannot happen with md finite)
+    const unsigned long long rem = L.uscratch[1];
+    const int s = hit / nsb, sbi = hit % nsb;
+    const int slo = s * G.slice_len, shi = min(R.V, slo + G.slice_len);
+    const Geo<2> g = slice_geo<2>(G, R.row, slo);
+    const int p0 = sbi * 512;  // positions [p0, p0 + 512) from g.first
+    // every load of the sub-block issued together: the slice's specials (all kSpecCap slots; the ones past nspec
+    // are dropped), and on wave 0 the logits and the mask words of lane l's 8 tokens
+    const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, s);
+    const unsigned long long* spl = (const unsigned long long*)((const char*)rec + kRecSpecOff);
+    constexpr int kSpecPer = kSpecCap / kThreads;
+    static_assert(kSpecPer * kThreads == kSpecCap, "specials per thread");
+    unsigned long long se[kSpecPer];
+    const int ns = min(pub_ld(&rec->nspec), kSpecCap);
+#pragma unroll
+    for (int q = 0; q < kSpecPer; ++q) se[q] = pub_ld(spl + q * kThreads + tid);
+    const int j0 = g.first + p0 + 8 * l;
+    const int ja = min(max(j0, slo), shi - 1), jb = min(max(j0 + 7, slo), shi - 1);
+    uint4 cv = make_uint4(0u, 0u, 0u, 0u);
+    uint32_t wa = ~0u, wb = ~0u;
+    if (wave_id() == 0) {
+        cv = load_chunk<2>(g, sbi * 64 + l, shi);
+        if (G.allowed) {
+            const auto aw = gp(G.allowed) + (int64_t)R.row * G.allowed_stride;
+            wa = aw[ja >> 5];
+            wb = aw[jb >> 5];
+        }
+    }
+    // the specials in the sub-block: their masses (or 0) and a mark that leaves them out of the logits, at
+    // [e][lane] for position 8 lane + e, so that wave 0 reads them without bank conflicts
+    unsigned long long* om = (unsigned long long*)&L.a;  // 512 masses
+    uint32_t* osp = (uint32_t*)(om + 512);                // 512 marks
+    if (tid < 512) {
+        om[tid] = 0ull;
+        osp[tid] = 0u;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kSpecPer; ++q) {
+        const unsigned long long e = se[q];
+        const uint32_t id = (uint32_t)(e >> 32);
+        const int pos = (int)(id & ~kSelOnlyBit) - g.first - p0;
+        if (q * kThreads + tid < ns && pos >= 0 && pos < 512) {
+            const float qv = __uint_as_float((uint32_t)e);
+            const int at = (pos & 7) * 64 + (pos >> 3);
+            om[at] = (!(id & kSelOnlyBit) && qv >= thr) ? efx(qv, md) : 0ull;
+            osp[at] = 1u;
+        }
+    }
+    if (tid == 0 && R.eos_rule != kEosNormal && G.eos >= slo && G.eos < shi) {
+        const int pos = G.eos - g.first - p0;
+        if (pos >= 0 && pos < 512) osp[(pos & 7) * 64 + (pos >> 3)] = 1u;  // its mass stays 0
+    }
+    if (tid == 0) L.uscratch[0] = (unsigned long long)(R.V - 1);
+    __syncthreads();
+    MIS_STAMP(20);
+    if (wave_id() == 0) {
+        const unsigned long long* lut = lut_of(L);
+        const uint32_t wv[4] = {cv.x, cv.y, cv.z, cv.w};
+        unsigned long long m[8];
+        uint32_t bits = 0u;  // plain survivors: in the slice, allowed, not special, x >= x0
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int j = j0 + e;
+            const uint32_t w = (j >> 5) == (ja >> 5) ? wa : wb;
+            const bool sp = osp[e * 64 + l] != 0u;
+            m[e] = sp ? om[e * 64 + l] : 0ull;
+            const float x = __uint_as_float(((wv[e >> 1] >> (16 * (e & 1))) & 0xffffu) << 16);
+            if (!sp && j >= slo && j < shi && ((w >> (j & 31)) & 1u) && x >= x0) bits |= 1u << e;
+        }
+        uint32_t lumps = 0u;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            if (bits & (1u << e)) m[e] = r2_mass(lut, (wv[e >> 1] >> (16 * (e & 1))) & 0xffffu, e, lumps);
+        while (lumps) {  // rare: values within 2^-7 of zero
+            const int e = __ffs(lumps) - 1;
+            lumps &= lumps - 1u;
+            m[e] = efx(to_q<2>(R, __uint_as_float(((wv[e >> 1] >> (16 * (e & 1))) & 0xffffu) << 16)), md);
+        }
+        unsigned long long sum = 0ull;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sum += m[e];
+        const unsigned long long incl = wave_incl_scan(sum);
+        const unsigned long long exl = incl - sum;
+        const bool mine = sum && exl < rem && rem <= incl;
+        if (mine) {
+            unsigned long long c = exl;
+            int hitj = j0 + 7;
+            for (int e = 0; e < 8; ++e) {
+                if (m[e] && c + m[e] >= rem) {
+                    hitj = j0 + e;
+                    break;
+                }
+                c += m[e];
+            }
+            L.uscratch[0] = (unsigned long long)hitj;
+        }
+    }
+    __syncthreads();
+    return (int64_t)L.uscratch[0];
+}
+
+
+// The second round's last workgroup: the draw from the sub-block sums, then outputs and state; thr, md, x0 and u
+// are in L.fscratch.  A row some slice of which gave up waiting comes out as PAD, with its state untouched and the
+// workspace's error word raised.
+__device__ __forceinline__ void r2_finish(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L, bool failed) {
+    if (failed && threadIdx.x == 0) {  // this workgroup may have given up before the decision came
+        const float* dat = (const float*)(row_line(A, R) + kLineDat);
+        L.fscratch[0] = pub_ld(dat);
+        L.fscratch[1] = pub_ld(dat + 1);
+    }
+    __syncthreads();
+    Outcome o;
+    o.thr = L.fscratch[0];
+    o.mdraw = L.fscratch[1];
+    const float x0 = L.fscratch[2], u = L.fscratch[3];
+    __syncthreads();
+    MIS_STAMP(30);
+    o.token = failed ? (int64_t)kPad : r2_draw(G, R, L, o.thr, o.mdraw, x0, u);
+    MIS_STAMP(8);
+    if (threadIdx.x == 0 && G.paths) {
+        atomicAdd(G.paths + MIS_PATH_HISTOGRAM, 1u);
+        if (failed) atomicAdd(G.paths + (MIS_WS_ERROR_OFFSET - MIS_WS_PATH_OFFSET) / 4, 1u);
+    }
+    if (R.want_out) write_outputs(G, R, L, o, false);
+    if (failed) {
+        if (threadIdx.x == 0 && G.tokens) gp(G.tokens)[R.row] = kPad;
+        return;
+    }
+    update_state(G, R, o.token);
+    MIS_STAMP(10);
+    MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)R.slice << 8) | 0x80u |
+                   (unsigned)MIS_PATH_HISTOGRAM);
+}
+
 // The row's last workgroup (or slice 0 of a forced row).
 __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L, bool forced) {
     Outcome o;
@@ -3787,10 +4020,6 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
         } else if (mode == kFull) {
             fin_full(G, R, L, o);
             path = MIS_PATH_FULL;
-        } else if (mode == kNucleus && nucleus_hist(R, G.es)) {
-            path = MIS_PATH_HISTOGRAM;
-            if (!fin_hist(G, R, L, o)) mode = kStream;
-            MIS_STAMP(9);
         } else if (mode == kTopK || mode == kNucleus) {
             path = MIS_PATH_CANDIDATES;
             if (!fin_sel(G, R, L, o)) mode = kStream;
@@ -3837,8 +4066,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const KernelArgs args)
     const DevGroup& G = A.g[gi];
     Row R;
     const int act = G.es == 2 ? run<2>(A, G, gi, row, slice, L, R) : run<4>(A, G, gi, row, slice, L, R);
-    if (act != kActNone) {
+    if (act == kActR2Draw || act == kActR2Failed) {
+        r2_finish(A, G, R, L, act == kActR2Failed);
+    } else if (act != kActNone) {
         if (act == kActForced) L.foreign = 0;
+        if (act == kActStream) L.foreign = 1;  // finalised from the logits alone
         finalize(G, R, L, act == kActForced);
     }
 }
