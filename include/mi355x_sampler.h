@@ -55,9 +55,10 @@ enum { MIS_E_ARG = 1, MIS_E_WORKSPACE = 2, MIS_E_UNSUPPORTED = 3 };
  * uint32 counter per finalisation path, incremented once per sampled row and never cleared by the library; a caller
  * that wants per-launch figures zeroes them before the launch.  Which path a row takes never changes its result. */
 #define MIS_WS_PATH_OFFSET 64
-/* Bytes [MIS_WS_ERROR_OFFSET, + 4): rows that came out as PAD because one of their slices gave up waiting (2 ms) for
- * its row's second round (a top-p row without top-k settled from value counts); never cleared by the library.  It
- * stays 0 unless the device stalls a workgroup for milliseconds. */
+/* Bytes [MIS_WS_ERROR_OFFSET, + 4): uint32 count of slice workgroups that gave up waiting (2 ms) for their row's
+ * finaliser (a top-p row without top-k settled from value counts); never cleared by the library.  When the one that
+ * gave up held the row's draw, the row came out as PAD with its state untouched.  It stays 0 unless the device
+ * stalls a workgroup for milliseconds. */
 #define MIS_WS_ERROR_OFFSET 128
 enum {
     MIS_PATH_GREEDY = 0,     /* first argmax from the slices' maxima */

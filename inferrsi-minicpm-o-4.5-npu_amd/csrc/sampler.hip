@@ -79,7 +79,9 @@ constexpr int kMaxSB = kWaves * kRounds;         // (wave, round) sub-blocks of 
 constexpr double kFx = 4398046511104.0;          // 2^42 fixed-point units of exp(q - max): V * 2^42 < 2^64
 constexpr int kLineBytes = 128;                  // a row's arrival word has a cache line of its own
 constexpr int64_t kHeaderBytes = 256;            // diagnostic counters (MIS_WS_PATH_OFFSET)
-static_assert(MIS_WS_PATH_OFFSET + 4 * MIS_PATH_COUNT <= kHeaderBytes, "workspace header");
+static_assert(MIS_WS_PATH_OFFSET + 4 * MIS_PATH_COUNT <= kHeaderBytes && MIS_WS_ERROR_OFFSET + 4 <= kHeaderBytes &&
+                  MIS_WS_PATH_OFFSET + 4 * MIS_PATH_COUNT <= MIS_WS_ERROR_OFFSET,
+              "workspace header");
 // Arrival words live at fixed offsets (they must read zero at every launch, whatever the previous launch's shape).
 constexpr int64_t kArriveBytes = (int64_t)kMaxRows * kLineBytes;
 constexpr int kPad = -1;
@@ -159,11 +161,16 @@ struct SliceRec {
     int32_t ncand[kSegs];
     int32_t nhigh;   // histogram path: the first nhigh published specials lie at or above the value gate
     unsigned long long tinyfx;  // sum of exp(q) in fixed point over the tiny-magnitude lumps of the histogram
+    int32_t nlump;              // histogram path: the tiny-magnitude values listed (bf16 patterns)
 };
 constexpr int64_t kRecHead = 256;
 static_assert(sizeof(SliceRec) <= kRecHead, "slice record");
 constexpr int64_t kRecSbOff = kRecHead;
 constexpr int64_t kRecCandOff = kRecSbOff + 8 * kMaxSB;
+// Histogram slices publish no candidates: the candidate area holds the bf16 patterns of their tiny-magnitude values
+// (the lumps next to zero) instead, for the draw's exact survivor mass.
+constexpr int64_t kRecLumpOff = kRecCandOff;
+constexpr int kLumpCap = 4096;
 // Nucleus histogram of a bf16 slice: one key per bf16 value with |x| in [2^-7, 2^8) (1,920 per sign), zero, the
 // tiny magnitudes of each sign (lumps) and the huge ones (lumps); keys increase with the value.
 constexpr int kKeys = 3845;
@@ -243,6 +250,7 @@ struct Lds {
     int32_t flags;
     int32_t is_last;
     int32_t nhi, nlo;  // slice phase of the histogram path: specials at or above the value gate, and below it
+    int32_t nlump;     // slice phase of the histogram path: tiny-magnitude values listed
     int32_t foreign;
     int32_t token;
     float fscratch[4];
@@ -814,90 +822,150 @@ __device__ __forceinline__ bool nucleus_hist(const Row& R, int es) {
     return es == 2 && R.mode == kNucleus && R.T >= kHistMinT;
 }
 
-// ------------------------------------------------------------------ the histogram path's second round
-//
-// After a top-p row's cut is settled from the value counts, the draw needs the survivor mass of every 512-value
-// sub-block of the row.  The row's slices other than the finaliser keep their tiles in registers and wait on the
-// row's line.  The finaliser first publishes the draw's reference md (the row's largest drawable value), and the
-// waiting slices build the table of masses by value (r2_lut) while it settles the cut; then it publishes the
-// decision, each slice sums its sub-blocks and counts itself in a second time, and the last to do so draws inside
-// the one sub-block that holds the target.  A waiting slice waits only for its row's finaliser, which has arrived
-// and is running, so the wait ends whatever the scheduling; a slice that still gives up (after kR2SpinTicks) counts
-// itself in with a failure mark, and the row then comes out as PAD, with the workspace's error word raised, and its
-// state untouched.
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long x, int lane);
+__device__ __forceinline__ void write_outputs(const DevGroup& G, const Row& R, Lds& L, const Outcome& o, bool forced);
+__device__ __forceinline__ void update_state(const DevGroup& G, const Row& R, int64_t tok);
 
-constexpr int kLineDec = 64;  // u32 on the row's line: 0 pending, 3 md published, 1 settled by the finaliser (the
-                              // row is streamed), 2 sub-block sums wanted
-constexpr int kLineR2 = 68;   // u32: second-round arrivals (low 16 bits) and failures (high 16 bits)
-constexpr int kLineDat = 72;  // f32 thr, md, x0 (the least bf16 value x with x / T >= thr), u (the row's uniform)
+// ------------------------------------------------------------------ the histogram path's draw
+//
+// After a top-p row's cut is settled from the value counts, the finaliser also has every slice's exact survivor mass
+// (its counts weighed by value, its listed tiny values, its drawable specials: the same integers the slice's own
+// elements sum to), so it knows which slice holds the draw's target and where the target lies in that slice's
+// survivor mass.  The row's other slices keep their tiles in registers and wait on the row's line; the finaliser
+// first publishes the draw's reference md (the row's largest drawable value), so that they build the table of masses
+// by value while it settles the cut, then the decision.  The slice that holds the target sums its 512-value
+// sub-blocks and draws inside one of them from its registers; the others leave.  A waiting slice waits only for
+// its row's finaliser, which has arrived and is running, so the wait ends whatever the scheduling; a slice that
+// still gives up (after kR2SpinTicks) raises the workspace's error word, and when it held the target the row comes
+// out as PAD (written by the finaliser before the decision) with its state untouched.
+
+constexpr int kLineDec = 64;   // u32 on the row's line: 0 pending, 3 md published, 1 settled by the finaliser (the
+                               // row is streamed), 2 drawn by the holder
+constexpr int kLineSeen = 68;  // u32: slices done with the line (the finaliser after its decision)
+constexpr int kLineDat = 72;   // f32 thr, md, x0 (the least bf16 value x with x / T >= thr)
+constexpr int kLineHolder = 84;  // u32: the slice that holds the target
+constexpr int kLineRem = 88;     // u64: the target within the holder's survivor mass (1-based)
 constexpr unsigned long long kR2SpinTicks = 200000ull;  // 2 ms of the 100 MHz real-time counter
-static_assert(kLineDat + 16 <= kLineBytes, "row line");
-// The mass table (kKeys + 1 entries of 8 bytes) lies in L.a past what the histogram finaliser keeps there (its
-// per-key tables, below 64 KB) and past a slice's counts, so a slice can build it before the cut is known.
-constexpr int kLutOff = 65536;
-static_assert(kLutOff + 8 * (kKeys + 1) <= (int)sizeof(Lds::a), "mass table");
-static_assert(16 * (kKeys + 1) + 12 * 256 <= kLutOff, "the histogram finaliser's tables");
+static_assert(kLineRem + 8 <= kLineBytes, "row line");
+
+// The holder's table of masses by bf16 value: entry kTabB + m for x >= 0 and kTabB - m for x < 0, where m = 0 for
+// |x| < 2^-15 (the entry holds zero's mass; the other values there are weighed one by one), m = 1 + a - kTabLo for
+// magnitude patterns a in [kTabLo, kBfHi), and m = kTabN for 256 and above, -inf and NaN (no mass: a row with
+// values of 256 and above is streamed, and values of -256 and below are never drawn here).  Values below x0 weigh
+// nothing.  The index is computed for two values at once in 16-bit lanes.
+constexpr uint32_t kTabLo = 0x3800u;                // 2^-15
+constexpr int kTabN = (int)(kBfHi - kTabLo) + 1;    // 2,945
+constexpr int kTabB = kTabN;
+constexpr int kTabSize = 2 * kTabN + 1;
+constexpr int kTabMarkOff = 8 * (kTabSize + 1);     // the draw's chunk marks follow the table in L.a
+constexpr int kChunkOff = 49152;                    // then the holder's chunk masses, [wave][round][lane]
+static_assert(kTabMarkOff + 8 * 12 <= kChunkOff && kChunkOff + 8 * kWaves * kRounds * 64 <= (int)sizeof(Lds::a),
+              "mass table");
+// The histogram finaliser keeps the first four slices' counts here (past its own tables, below 64 KB) for the
+// draw's survivor masses.
+constexpr int kStageOff = 65536;
+static_assert(16 * (kKeys + 1) + 12 * 256 <= kStageOff && kStageOff + 16 * kHistWords <= (int)sizeof(Lds::a),
+              "the histogram finaliser's tables and staged counts");
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ char* row_line(const KernelArgs& A, const Row& R) {
     return A.arrive + (int64_t)R.grow * kLineBytes;
 }
 
-// The finaliser's words to the waiting slices (thread 0): dec 3 with md, then 1, or 2 with thr, md, x0, u.
+__device__ __forceinline__ unsigned long long* tab_of(Lds& L) { return (unsigned long long*)&L.a; }
+
+// The table indexes of the two bf16 values of word v (low half: the lower element), and in tiny their magnitude
+// patterns minus one (below kTabLo - 1 exactly for a magnitude in (0, 2^-15)).
+__device__ __forceinline__ uint32_t tab_idx2(uint32_t v, uint32_t& tiny) {
+    const u16x2 w = __builtin_bit_cast(u16x2, v);
+    const u16x2 sg = __builtin_bit_cast(u16x2, __builtin_bit_cast(i16x2, v) >> (i16x2)15);  // 0xffff: negative
+    const u16x2 a = w & (u16x2)0x7fff;
+    u16x2 t = __builtin_elementwise_max(a, (u16x2)(kTabLo - 1));
+    t = __builtin_elementwise_min(t, (u16x2)kBfHi);
+    const u16x2 m = t - (u16x2)(kTabLo - 1);
+    const u16x2 idx = ((m ^ sg) - sg) + (u16x2)kTabB;
+    tiny = __builtin_bit_cast(uint32_t, a - (u16x2)1);
+    return __builtin_bit_cast(uint32_t, idx);
+}
+
+// The bf16 value of table entry i (0 for the entry of zero; not called for the huge entries).
+__device__ __forceinline__ float tab_val(int i) {
+    const int d = i - kTabB;
+    const uint32_t m = (uint32_t)(d < 0 ? -d : d);
+    if (m == 0u) return 0.0f;
+    const uint32_t b = (kTabLo - 1u + m) | (d < 0 ? 0x8000u : 0u);
+    return __uint_as_float(b << 16);
+}
+
+// The table (every thread): efx(x / T, md) for the values x >= x0 with x / T <= md, 0 elsewhere.
+__device__ __forceinline__ void r2_tab(const Row& R, Lds& L, float md, float x0) {
+    unsigned long long* tab = tab_of(L);
+    for (int i = threadIdx.x; i < kTabSize; i += kThreads) {
+        unsigned long long v = 0ull;
+        const int d = i - kTabB;
+        if (d > -kTabN && d < kTabN) {
+            const float x = tab_val(i);
+            const float q = to_q<2>(R, x);
+            if (x >= x0 && q <= md) v = efx(q, md);
+        }
+        tab[i] = v;
+    }
+}
+
+// The values below x0 out of a table built without a bound.
+__device__ __forceinline__ void r2_tab_cut(Lds& L, float x0) {
+    unsigned long long* tab = tab_of(L);
+    for (int i = threadIdx.x; i < kTabSize; i += kThreads) {
+        const int d = i - kTabB;
+        if (d > -kTabN && d < kTabN && tab_val(i) < x0) tab[i] = 0ull;
+    }
+}
+
+// The finaliser's words (thread 0): dec 3 with md, then 1, or 2 with thr, md, x0, the holder and the target.
 __device__ __forceinline__ void r2_decide(const KernelArgs& A, const Row& R, unsigned dec, float thr, float md, float x0,
-                                          float u) {
+                                          int holder, unsigned long long rem) {
     if (threadIdx.x != 0) return;
     char* line = row_line(A, R);
     float* d = (float*)(line + kLineDat);
     if (dec == 2u) {
         d[0] = thr;
         d[2] = x0;
-        d[3] = u;
+        *(uint32_t*)(line + kLineHolder) = (uint32_t)holder;
+        *(unsigned long long*)(line + kLineRem) = rem;
     }
-    if (dec != 1u) {
-        d[1] = md;
-        wait_stores();
-    }
+    if (dec != 1u) d[1] = md;
+    wait_stores();
     __hip_atomic_store((unsigned*)(line + kLineDec), dec, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ int lut_key(uint32_t b) {  // the exact key of bf16 pattern b, or kKeys for a lump
-    const uint32_t a = b & 0x7fffu;
-    const uint32_t m = a - kBfLo;
-    const int k = (b & 0x8000u) ? kKeyZero - 2 - (int)m : kKeyZero + 2 + (int)m;
-    return a == 0u ? kKeyZero : (m < kBfHi - kBfLo ? k : kKeys);
-}
-
-__device__ __forceinline__ unsigned long long* lut_of(Lds& L) {
-    return (unsigned long long*)((char*)&L.a + kLutOff);
-}
-
-// The masses by value (every thread): lut[k] = efx(x / T, md) for every exact histogram key k with x / T <= md
-// (x its bf16 value), 0 for the others and at lut[kKeys], which every lump maps to: a lump's values differ from one
-// another, so they are weighed one by one.
-__device__ __forceinline__ void r2_lut(const Row& R, Lds& L, float md) {
-    unsigned long long* lut = lut_of(L);
-    for (int k = threadIdx.x; k <= kKeys; k += kThreads) {
-        unsigned long long v = 0ull;
-        if (key_exact(k)) {
-            const float q = to_q<2>(R, key_bf(k));
-            if (q <= md) v = efx(q, md);
-        }
-        lut[k] = v;
-    }
-}
-
-// A waiting slice: the decision (0 if it gave up waiting), with thr, md, x0, u in L.fscratch when it is 2; the mass
-// table is built on the way, as soon as md is out.
-__device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, Lds& L) {
+// A slice done with the row's line (thread 0; the finaliser once its decision is out): the last of the row's
+// slices leaves the words zero for the next launch.  A slice that gave up raises the workspace's error word.
+__device__ __forceinline__ void r2_seen(const KernelArgs& A, const DevGroup& G, const Row& R, bool gave_up) {
+    if (threadIdx.x != 0) return;
     char* line = row_line(A, R);
+    unsigned* sw = (unsigned*)(line + kLineSeen);
+    const unsigned now = __hip_atomic_fetch_add(sw, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    if ((int)now == R.S) {
+        __hip_atomic_store((unsigned*)(line + kLineDec), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (gave_up && G.paths) atomicAdd(G.paths + (MIS_WS_ERROR_OFFSET - MIS_WS_PATH_OFFSET) / 4, 1u);
+}
+
+// A waiting slice: the decision (0 if it gave up waiting).  With 2, L.fscratch holds thr, md, x0, L.scnt the holder
+// and L.uscratch[0] the target; the table is built on the way (without its bound x0), as soon as md is out.
+__device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, Lds& L) {
+    const char* line = row_line(A, R);
     unsigned* dw = (unsigned*)(line + kLineDec);
     const float* dat = (const float*)(line + kLineDat);
     const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
-    bool have_lut = false;
+    bool have_tab = false;
     for (;;) {
         if (threadIdx.x == 0) {
             unsigned d = __hip_atomic_load(dw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            while (d == 0u || (have_lut && d == 3u)) {
+            while (d == 0u || (have_tab && d == 3u)) {
                 if (__builtin_amdgcn_s_memrealtime() - t0 > kR2SpinTicks) {
                     d = 0u;
                     break;
@@ -908,7 +976,8 @@ __device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, L
             if (d == 2u) {
                 L.fscratch[0] = pub_ld(dat);
                 L.fscratch[2] = pub_ld(dat + 2);
-                L.fscratch[3] = pub_ld(dat + 3);
+                L.scnt = (int)pub_ld((const uint32_t*)(line + kLineHolder));
+                L.uscratch[0] = pub_ld((const unsigned long long*)(line + kLineRem));
             }
             if (d >= 2u) L.fscratch[1] = pub_ld(dat + 1);
             L.token = (int)d;
@@ -916,98 +985,13 @@ __device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, L
         __syncthreads();
         const unsigned d = (unsigned)L.token;
         if (d == 0u || d == 1u) return d;
-        if (!have_lut) {
-            r2_lut(R, L, L.fscratch[1]);
-            have_lut = true;
+        if (!have_tab) {
+            r2_tab(R, L, L.fscratch[1], -INFINITY);
+            have_tab = true;
         }
         __syncthreads();  // the table complete, and L.token read by every thread before thread 0 writes it again
         if (d == 2u) return d;
     }
-}
-
-// Second-round arrival (every thread): true in the row's last workgroup, which also gets the decision as it stood
-// and whether some slice gave up; the last one leaves the row's words zero for the next launch.
-__device__ __forceinline__ bool r2_arrive(const KernelArgs& A, const Row& R, Lds& L, bool gave_up, unsigned& dec,
-                                          bool& failed) {
-    wait_stores();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        char* line = row_line(A, R);
-        unsigned* w2 = (unsigned*)(line + kLineR2);
-        unsigned* dw = (unsigned*)(line + kLineDec);
-        const unsigned add = 1u + (gave_up ? 0x10000u : 0u);
-        const unsigned now = __hip_atomic_fetch_add(w2, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
-        const int last = (int)(now & 0xffffu) == R.S;
-        unsigned d = 0u;
-        if (last) {
-            d = __hip_atomic_load(dw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(dw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(w2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        L.is_last = last;
-        L.foreign = (now >> 16) != 0u ? 1 : 0;
-        L.flags = (int)d;
-    }
-    __syncthreads();
-    dec = (unsigned)L.flags;
-    failed = L.foreign != 0;
-    return L.is_last != 0;
-}
-
-// The mass of one surviving tile element (bf16 pattern b): the table's, or 0 with its bit in `lumps` when b is a
-// lump value, which the caller weighs with efx.
-__device__ __forceinline__ unsigned long long r2_mass(const unsigned long long* lut, uint32_t b, int e,
-                                                      uint32_t& lumps) {
-    const int k = lut_key(b);
-    if (k == kKeys) lumps |= 1u << e;
-    return lut[k];
-}
-
-// The survivor mass of every (wave, round) sub-block of a bf16 tile (masked values -inf) and of the slice's
-// specials in L.spec (ns of them), published to the slice's record.  Survivors: x >= x0 (q = x / T >= thr), and the
-// drawable specials with q >= thr.  The mass table must be built.
-__device__ __forceinline__ void r2_sums(const DevGroup& G, const Row& R, Lds& L, const uint4 (&t)[kRounds], int RR,
-                                        int first, int ns, float thr, float md, float x0) {
-    const int tid = threadIdx.x, w = wave_id(), l = lane_id();
-    const unsigned long long* lut = lut_of(L);
-    if (tid < kMaxSB) L.sbfx[tid] = 0ull;
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < kRounds; ++r) {
-        if (r >= RR) continue;
-        // the survivors as a mask first: the table is read for them alone
-        uint32_t bits = 0u;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) bits |= tile_val<2>(t[r], e) >= x0 ? (1u << e) : 0u;
-        unsigned long long acc = 0ull;
-        if (ballot(bits != 0u)) {
-            uint32_t lumps = 0u;
-            while (bits) {
-                const int e = __ffs(bits) - 1;
-                bits &= bits - 1u;
-                acc += r2_mass(lut, __float_as_uint(tile_val_dyn<2>(t[r], e)) >> 16, e, lumps);
-            }
-            if (ballot(lumps != 0u)) {  // rare: values within 2^-7 of zero
-                while (lumps) {
-                    const int e = __ffs(lumps) - 1;
-                    lumps &= lumps - 1u;
-                    acc += efx(to_q<2>(R, tile_val_dyn<2>(t[r], e)), md);
-                }
-            }
-            acc = wave_reduce(acc, [](unsigned long long a, unsigned long long b) { return a + b; });
-        }
-        if (l == 0) L.sbfx[w * RR + r] = acc;
-    }
-    __syncthreads();
-    MIS_STAMP(17);
-    for (int i = tid; i < ns; i += kThreads) {
-        const Special sp = L.spec[i];
-        if (!sp.sel && sp.q >= thr) atomicAdd(&L.sbfx[(sp.j - first) >> 9], efx(sp.q, md));
-    }
-    __syncthreads();
-    MIS_STAMP(18);
-    unsigned long long* sb = (unsigned long long*)(rec_base(G, R.row, R.slice) + kRecSbOff);
-    if (tid < kWaves * RR) sb[tid] = L.sbfx[tid];
 }
 
 // The least bf16 value x with x / T >= thr (finite thr), the same in every lane of the calling wave: x0 lies within
@@ -1034,10 +1018,161 @@ __device__ __forceinline__ float r2_x0(const Row& R, float thr) {
     return val(hi);
 }
 
-__device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
-                                        Outcome& out, float& u);
+// The mass of the 8 bf16 values of chunk v (survivors: x >= x0, by the table; the tiny ones weighed here), into m[].
+__device__ __forceinline__ void r2_chunk_masses(const Row& R, const unsigned long long* tab, const uint4& v, float x0,
+                                                float md, unsigned long long (&m)[8]) {
+    const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+    uint32_t tmin = 0xffffffffu;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        uint32_t tn;
+        const uint32_t ix = tab_idx2(wv[h], tn);
+        tmin = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, tmin),
+                                                                       __builtin_bit_cast(u16x2, tn)));
+        m[2 * h] = tab[ix & 0xffffu];
+        m[2 * h + 1] = tab[ix >> 16];
+    }
+    const bool tiny = (tmin & 0xffffu) < kTabLo - 1u || (tmin >> 16) < kTabLo - 1u;
+    if (ballot(tiny)) {  // rare: magnitudes in (0, 2^-15)
+        if (tiny) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t b = (wv[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                const uint32_t a = b & 0x7fffu;
+                const float x = __uint_as_float(b << 16);
+                if (a != 0u && a < kTabLo) m[e] = x >= x0 ? efx(to_q<2>(R, x), md) : 0ull;
+            }
+        }
+    }
+}
 
-enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2, kActR2Draw = 3, kActR2Failed = 4, kActStream = 5 };
+// The holder's draw.  Each lane's survivor mass per round (the 8 values of one 16-byte chunk) goes to LDS and the
+// wave's total to one reduction; each drawable special's mass is added to its chunk and its wave.  Wave 0 then
+// finds the wave that holds the target, that wave the chunk (a scan over its lanes, round by round: chunks are in
+// token order), and the chunk's lane the token.  The table must be built with its bound.
+__device__ __forceinline__ int64_t r2_hold(const Row& R, Lds& L, const uint4 (&t)[kRounds], int RR, int first, int ns,
+                                           float thr, float md, float x0, unsigned long long rem) {
+    const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+    const unsigned long long* tab = tab_of(L);
+    unsigned long long* cs = (unsigned long long*)((char*)&L.a + kChunkOff);  // [wave][round][lane]
+    unsigned long long tot = 0ull;
+#pragma unroll
+    for (int r = 0; r < kRounds; ++r) {
+        if (r >= RR) continue;
+        unsigned long long m[8];
+        r2_chunk_masses(R, tab, t[r], x0, md, m);
+        unsigned long long c = 0ull;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) c += m[e];
+        cs[(w * kRounds + r) * 64 + l] = c;
+        tot += c;
+    }
+    tot = wave_reduce(tot, [](unsigned long long a, unsigned long long b) { return a + b; });
+    if (l == 0) L.sbfx[w] = tot;
+    __syncthreads();
+    MIS_STAMP(17);
+    // the specials (their chunks marked in L.keep, which the tile no longer needs)
+    uint32_t* smark = L.keep;
+    for (int i = tid; i < kKeepWords; i += kThreads) smark[i] = 0u;
+    __syncthreads();
+    for (int i = tid; i < ns; i += kThreads) {
+        const Special sp = L.spec[i];
+        const int c = (sp.j - first) >> 3;  // chunk (w RR + r) 64 + l
+        atomicOr(&smark[c >> 5], 1u << (c & 31));
+        if (!sp.sel && sp.q >= thr) {
+            const int sw = c / (RR * 64), sr = (c >> 6) % RR;
+            const unsigned long long f = efx(sp.q, md);
+            atomicAdd(&cs[(sw * kRounds + sr) * 64 + (c & 63)], f);
+            atomicAdd(&L.sbfx[sw], f);
+        }
+    }
+    if (tid == 0) L.scnt = -1;
+    __syncthreads();
+    MIS_STAMP(18);
+    // the wave of the target (every wave finds it), then that wave's chunk, round by round
+    int hw;
+    unsigned long long rw;
+    {
+        const unsigned long long v = l < kWaves ? L.sbfx[l] : 0ull;
+        const unsigned long long incl = wave_incl_scan(v);
+        const uint64_t h = ballot(l < kWaves && incl >= rem);
+        hw = h ? __ffsll((long long)h) - 1 : -1;
+        rw = hw >= 0 ? rem - (readlane_u64(incl, hw) - readlane_u64(v, hw)) : 0ull;
+    }
+    if (hw < 0) return R.V - 1;  // cannot happen: rem is at most the holder's survivor mass
+    if (w == hw) {
+        unsigned long long rr = rw;
+        for (int r = 0; r < RR; ++r) {
+            const unsigned long long v = cs[(w * kRounds + r) * 64 + l];
+            const unsigned long long incl = wave_incl_scan(v);
+            const unsigned long long wt = readlane_u64(incl, 63);
+            if (rr <= wt) {
+                const uint64_t h = ballot(incl >= rr);
+                if (l == __ffsll((long long)h) - 1) {
+                    L.scnt = r * 64 + l;
+                    L.uscratch[0] = rr - (incl - v);
+                }
+                break;
+            }
+            rr -= wt;
+        }
+    }
+    __syncthreads();
+    const int hc = L.scnt;
+    if (hc < 0) return R.V - 1;
+    const int hr = hc >> 6, hl = hc & 63;
+    const int hcc = (hw * RR + hr) * 64 + hl;  // the chunk
+    const int pos0 = hcc * 8;                  // its first position from first
+    // the chunk's specials, when it has any: their masses (or 0), and marks that leave them out of the tile
+    unsigned long long* om = (unsigned long long*)((char*)&L.a + kTabMarkOff);
+    uint32_t* osp = (uint32_t*)(om + 8);
+    const bool has_spec = (smark[hcc >> 5] >> (hcc & 31)) & 1u;
+    if (tid < 8) {
+        om[tid] = 0ull;
+        osp[tid] = 0u;
+    }
+    if (tid == 0) L.uscratch[1] = (unsigned long long)(R.V - 1);
+    if (has_spec) {
+        __syncthreads();
+        for (int i = tid; i < ns; i += kThreads) {
+            const Special sp = L.spec[i];
+            const int pos = sp.j - first - pos0;
+            if (pos >= 0 && pos < 8) {
+                om[pos] = (!sp.sel && sp.q >= thr) ? efx(sp.q, md) : 0ull;
+                osp[pos] = 1u;
+            }
+        }
+    }
+    __syncthreads();
+    MIS_STAMP(19);
+    if (w == hw && l == hl) {
+        const unsigned long long rc = L.uscratch[0];
+#pragma unroll
+        for (int r = 0; r < kRounds; ++r) {  // a constant index into the tile, which stays in registers
+            if (r >= RR || r != hr) continue;
+            unsigned long long m[8];
+            r2_chunk_masses(R, tab, t[r], x0, md, m);
+            unsigned long long c = 0ull;
+            int last = -1;
+            for (int e = 0; e < 8; ++e) {
+                if (osp[e]) m[e] = om[e];  // a special's tile value is -inf: its mass comes from the list
+                if (!m[e]) continue;
+                last = e;
+                if (c + m[e] >= rc) break;
+                c += m[e];
+            }
+            if (last >= 0) L.uscratch[1] = (unsigned long long)(first + pos0 + last);
+        }
+    }
+    __syncthreads();
+    MIS_STAMP(20);
+    return (int64_t)L.uscratch[1];
+}
+
+__device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
+                                        Outcome& out, float& x0, int& holder, unsigned long long& rem);
+
+enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2, kActStream = 3 };
 
 // One slice workgroup: loads, the row's pipeline on the tile, publication, arrival.  Returns kActFinalize in the
 // row's last workgroup to arrive (R then holds the row), kActForced in slice 0 of a row whose EOS is forced.
@@ -1287,10 +1422,12 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 L.tinyfx = 0ull;
                 L.nhi = 0;
                 L.nlo = 0;
+                L.nlump = 0;
             }
             __syncthreads();
             MIS_STAMP(26);
             uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
+            uint32_t* lumps = (uint32_t*)((char*)rec + kRecLumpOff);
             unsigned long long tf = 0ull;
             // sum of exp(q - mq) over what is left out, as 2^(x log2(e) / T - mq log2(e)) in float: these masses
             // sum to at most V e^-D of the row's largest, so their relative error of a few 1e-6 stays far below
@@ -1309,8 +1446,11 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                     if (x >= g_raw) {
                         const int k = bf_key(b);
                         atomicAdd(&hk[k], 1u);
-                        if (k == kKeyZero - 1 || k == kKeyZero + 1)
+                        if (k == kKeyZero - 1 || k == kKeyZero + 1) {
                             tf += (unsigned long long)((double)exp_acc(to_q<2>(R, x)) * kFx);
+                            const int slot = atomicAdd(&L.nlump, 1);
+                            if (slot < kLumpCap) lumps[slot] = b;
+                        }
                     } else if (x == x) {
                         zr += __builtin_amdgcn_exp2f(__builtin_fmaf(x, c1, -c2));
                     }
@@ -1363,46 +1503,64 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 rec->gate = hb;
                 rec->mref = mq;
                 rec->z = z;
-                rec->flags = L.flags;
+                rec->flags = L.flags | (L.nlump > kLumpCap ? kRecOverflow : 0);
                 rec->hist = 1;
                 rec->nspec = ns;
                 rec->nhigh = L.nhi;
                 rec->tinyfx = L.tinyfx;
+                rec->nlump = min(L.nlump, kLumpCap);
             }
-            unsigned dec;
-            bool failed;
-            if (!arrive(A, R, L)) {
-                // held for the second round, the tile still in registers
+            Outcome o;
+            float x0 = 0.f;
+            unsigned long long rem = 0ull;
+            const bool fin = arrive(A, R, L);
+            if (!fin) {
+                // held, the tile in registers, until the finaliser's decision; the slice that holds the draw's
+                // target draws it
                 const unsigned d = r2_wait(A, R, L);
                 MIS_STAMP(9);
-                if (d == 2u) r2_sums(G, R, L, t, RR, geo.first, ns, L.fscratch[0], L.fscratch[1], L.fscratch[2]);
-                MIS_STAMP(15);
-                if (r2_arrive(A, R, L, d == 0u, dec, failed) && dec == 2u) return failed ? kActR2Failed : kActR2Draw;
-                return kActNone;
+                if (d != 2u || L.scnt != R.slice) {
+                    r2_seen(A, G, R, d == 0u);
+                    return kActNone;
+                }
+                o.thr = L.fscratch[0];
+                o.mdraw = L.fscratch[1];
+                x0 = L.fscratch[2];
+                rem = L.uscratch[0];
+                r2_tab_cut(L, x0);
+            } else {
+                // the row's finaliser, its tile still in registers: the cut and the target's slice from every
+                // slice's counts
+                int holder = -1;
+                const int res = L.foreign ? 0 : fin_hist(A, G, R, L, o, x0, holder, rem);
+                MIS_STAMP(9);
+                if (res != 2) {  // the row is streamed: the waiting slices are released
+                    if (R.S > 1) {
+                        r2_decide(A, R, 1u, 0.f, 0.f, 0.f, 0, 0ull);
+                        r2_seen(A, G, R, false);
+                    }
+                    return kActStream;
+                }
+                if (R.S > 1) {
+                    if (holder != R.slice && tid == 0 && G.tokens) gp(G.tokens)[R.row] = kPad;  // the holder's later
+                    r2_decide(A, R, 2u, o.thr, o.mdraw, x0, holder, rem);
+                }
+                if (tid == 0 && G.paths) atomicAdd(G.paths + MIS_PATH_HISTOGRAM, 1u);
+                if (holder != R.slice) {
+                    if (R.want_out) write_outputs(G, R, L, o, false);
+                    if (R.S > 1) r2_seen(A, G, R, false);
+                    return kActNone;
+                }
+                r2_tab(R, L, o.mdraw, x0);
             }
-            // the row's finaliser, its tile still in registers: the cut from every slice's counts, then its own
-            // sub-block sums like the others'
-            Outcome o;
-            float u = 0.f;
-            const int res = L.foreign ? 0 : fin_hist(A, G, R, L, o, u);
-            MIS_STAMP(9);
-            if (res != 2) {  // the row is streamed (or has no survivor): the waiting slices are released
-                r2_decide(A, R, 1u, 0.f, 0.f, 0.f, 0.f);
-                (void)r2_arrive(A, R, L, false, dec, failed);
-                return kActStream;
-            }
-            const float x0 = r2_x0(R, o.thr);
-            r2_decide(A, R, 2u, o.thr, o.mdraw, x0, u);
-            if (tid == 0) {  // for r2_finish, as a waiting slice has them
-                L.fscratch[0] = o.thr;
-                L.fscratch[1] = o.mdraw;
-                L.fscratch[2] = x0;
-                L.fscratch[3] = u;
-            }
-            MIS_STAMP(14);
-            r2_sums(G, R, L, t, RR, geo.first, ns, o.thr, o.mdraw, x0);
-            MIS_STAMP(15);
-            if (r2_arrive(A, R, L, false, dec, failed) && dec == 2u) return failed ? kActR2Failed : kActR2Draw;
+            __syncthreads();
+            o.token = r2_hold(R, L, t, RR, geo.first, ns, o.thr, o.mdraw, x0, rem);
+            if (fin && R.want_out) write_outputs(G, R, L, o, false);
+            update_state(G, R, o.token);
+            if (R.S > 1) r2_seen(A, G, R, false);  // after the draw: its wait is off the path
+            MIS_STAMP(10);
+            MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)R.slice << 8) | 0x80u |
+                           (unsigned)MIS_PATH_HISTOGRAM);
             return kActNone;
         }
     }
@@ -3370,9 +3528,9 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
 // False: the row is streamed instead.
 // 0: the row must be streamed; 1: no survivor; 2: the cut (out.thr, out.mdraw) for the second round.
 __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L, Outcome& out,
-                                        float& u) {
+                                        float& x0, int& holder, unsigned long long& rem) {
     const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
-    if (tid == 0) L.fscratch[3] = row_uniform(G, R);  // the draw's, for the second round
+    if (tid == 0) L.fscratch[3] = row_uniform(G, R);  // the draw's
     if (w == 0) {  // lane s reads slice s's record
         float mq = -INFINITY, mqd = -INFINITY, mr = -INFINITY, hb = -INFINITY;
         double zz = 0.0;
@@ -3422,9 +3580,9 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
     out.mdraw = -INFINITY;
     out.token = R.V - 1;
     if (!(m > -INFINITY)) return 1;
-    u = L.fscratch[3];
+    const float u = L.fscratch[3];
     // md to the waiting slices, which build their mass tables while the cut is settled here
-    if (mdraw > -INFINITY) r2_decide(A, R, 3u, 0.f, mdraw, 0.f, 0.f);
+    if (S > 1 && mdraw > -INFINITY) r2_decide(A, R, 3u, 0.f, mdraw, 0.f, 0, 0ull);
     // every slice's counts, merged: the first four slices' loads are in flight while the mass table is built
     uint32_t* cnt = (uint32_t*)L.h.w;
     constexpr int kMI = (kHistWords + kThreads - 1) / kThreads;
@@ -3438,7 +3596,8 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
                              ? pub_ld((const uint32_t*)(rec_base(G, R.row, u4) + kRecHistOff) + i)
                              : 0u;
     }
-    if (mdraw > -INFINITY) r2_lut(R, L, mdraw);
+    // the first four slices' counts also stay in LDS, for the draw's survivor masses
+    uint32_t* stc = (uint32_t*)((char*)&L.a + kStageOff);
 #pragma unroll
     for (int mi = 0; mi < kMI; ++mi) {
         const int i = mi * kThreads + tid;
@@ -3447,6 +3606,7 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
         for (int u4 = 0; u4 < 4; ++u4) {
             a += hv[mi][u4] & 0xffffu;
             b += hv[mi][u4] >> 16;
+            if (i < kHistWords) stc[u4 * kHistWords + i] = hv[mi][u4];
         }
         for (int s0 = 4; s0 < S; s0 += 4) {
             uint32_t v[4];
@@ -3659,13 +3819,152 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
             vmk = -INFINITY;
         }
     }
-    const float q_tlo = to_q<2>(R, -0.0078125f);
     const float thr = fminf(thr_p, vmk);
     if (!(thr > hbound)) return 0;
     const float md = mdraw >= thr ? mdraw : -INFINITY;
     out.thr = thr;
     out.mdraw = md;
-    return md > -INFINITY ? 2 : 1;
+    if (!(md > -INFINITY)) return 1;
+    MIS_STAMP(13);
+    // the draw's target: every slice's survivor mass (its counted values by key, its listed tiny values, its
+    // drawable specials: the integers its own elements sum to), then the slice that holds the target and the target
+    // within that slice's mass
+    x0 = r2_x0(R, thr);
+    const int k0 = bf_key(__float_as_uint(x0) >> 16);
+    if (k0 == 0 && cnt[0] != 0u) return 0;  // values of -256 and below may survive: not resolved here
+    MIS_STAMP(15);
+    if (tid < kMaxSlices) L.slice_u[tid] = 0ull;
+    // the loads first, together: the first four slices' list lengths and first entries, this thread's first four
+    // specials at or above the gate (segment s of the list is slice s's); all addresses in bounds
+    auto spec_slice = [&](int i) {
+        int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (L.segoff[mid] <= i)
+                lo = mid;
+            else
+                hi = mid;
+        }
+        return lo;
+    };
+    auto spec_mass = [&](unsigned long long e) -> unsigned long long {
+        const float q = __uint_as_float((uint32_t)e);
+        return (!((uint32_t)(e >> 32) & kSelOnlyBit) && q >= thr) ? efx(q, md) : 0ull;
+    };
+    const char* rb0 = rec_base(G, R.row, 0);
+    int nl[4];
+    uint32_t lv[4];
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+        const char* rb = rb0 + (int64_t)min(u4, S - 1) * kRecBytes;
+        nl[u4] = pub_ld(&((const SliceRec*)rb)->nlump);
+        lv[u4] = pub_ld((const uint32_t*)(rb + kRecLumpOff) + tid);
+    }
+    int ssl[4];
+    unsigned long long se[4];
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+        const int i = u4 * kThreads + tid;
+        const int ic = i < ntot ? i : 0;
+        const int sl = spec_slice(ic);
+        se[u4] = pub_ld((const unsigned long long*)(rb0 + (int64_t)sl * kRecBytes + kRecSpecOff) + (ic - L.segoff[sl]));
+        ssl[u4] = i < ntot ? sl : -1;
+    }
+    // the masses of this thread's keys 2 i and 2 i + 1 (the loads land meanwhile)
+    unsigned long long mk[kMI][2];
+#pragma unroll
+    for (int mi = 0; mi < kMI; ++mi)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = 2 * (mi * kThreads + tid) + h;
+            mk[mi][h] = 0ull;
+            if (k >= k0 && k < kKeys && key_exact(k)) mk[mi][h] = efx(to_q<2>(R, key_bf(k)), md);
+        }
+    __syncthreads();  // L.slice_u cleared
+    MIS_STAMP(16);
+    // the first four slices in registers: counts by key, listed tiny values, specials
+    unsigned long long z4[4];
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+        z4[u4] = 0ull;
+        if (u4 >= S) continue;
+#pragma unroll
+        for (int mi = 0; mi < kMI; ++mi) {
+            const int i = mi * kThreads + tid;
+            const uint32_t c = i < kHistWords ? stc[u4 * kHistWords + i] : 0u;
+            z4[u4] += (unsigned long long)(c & 0xffffu) * mk[mi][0] + (unsigned long long)(c >> 16) * mk[mi][1];
+        }
+        const uint32_t* lst = (const uint32_t*)(rb0 + (int64_t)u4 * kRecBytes + kRecLumpOff);
+        for (int i = tid; i < nl[u4]; i += kThreads) {
+            const float x = __uint_as_float((i == tid ? lv[u4] : pub_ld(lst + i)) << 16);
+            if (x >= x0) z4[u4] += efx(to_q<2>(R, x), md);
+        }
+    }
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+        if (ssl[u4] < 0) continue;
+        const unsigned long long f = spec_mass(se[u4]);
+        if (ssl[u4] >= 4) {
+            if (f) atomicAdd(&L.slice_u[ssl[u4]], f);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (ssl[u4] == q) z4[q] += f;
+        }
+    }
+    for (int i = 4 * kThreads + tid; i < ntot; i += kThreads) {  // more than 4,096 specials at or above the gate
+        const int sl = spec_slice(i);
+        const unsigned long long f =
+            spec_mass(pub_ld((const unsigned long long*)(rb0 + (int64_t)sl * kRecBytes + kRecSpecOff) + (i - L.segoff[sl])));
+        if (f) atomicAdd(&L.slice_u[sl], f);
+    }
+    MIS_STAMP(21);
+#pragma unroll
+    for (int u4 = 0; u4 < 4; ++u4) {
+        if (u4 >= S) break;
+        const unsigned long long z = wave_reduce(z4[u4], [](unsigned long long a, unsigned long long b) { return a + b; });
+        if (l == 0 && z) atomicAdd(&L.slice_u[u4], z);
+    }
+    // slices 4 and on (vocabularies above four slices): counts and lists from their records
+    for (int s4 = 4; s4 < S; ++s4) {
+        const char* rb = rb0 + (int64_t)s4 * kRecBytes;
+        unsigned long long z = 0ull;
+#pragma unroll
+        for (int mi = 0; mi < kMI; ++mi) {
+            const int i = mi * kThreads + tid;
+            const uint32_t c = i < kHistWords ? pub_ld((const uint32_t*)(rb + kRecHistOff) + i) : 0u;
+            z += (unsigned long long)(c & 0xffffu) * mk[mi][0] + (unsigned long long)(c >> 16) * mk[mi][1];
+        }
+        const int n = pub_ld(&((const SliceRec*)rb)->nlump);
+        for (int i = tid; i < n; i += kThreads) {
+            const float x = __uint_as_float(pub_ld((const uint32_t*)(rb + kRecLumpOff) + i) << 16);
+            if (x >= x0) z += efx(to_q<2>(R, x), md);
+        }
+        z = wave_reduce(z, [](unsigned long long a, unsigned long long b) { return a + b; });
+        if (l == 0 && z) atomicAdd(&L.slice_u[s4], z);
+    }
+    MIS_STAMP(24);
+    __syncthreads();
+    if (w == 0) {
+        const unsigned long long zs = l < S ? L.slice_u[l] : 0ull;
+        const unsigned long long incl = wave_incl_scan(zs);
+        const unsigned long long Z = readlane_u64(incl, 63);
+        int hs = -1;
+        unsigned long long T2 = 0ull;
+        if (Z) {
+            const double pt = floor((double)u * (double)Z) + 1.0;
+            T2 = pt >= (double)Z ? Z : (unsigned long long)pt;
+            const uint64_t h = ballot(incl >= T2);
+            hs = __ffsll((long long)h) - 1;
+            if (l == hs) L.uscratch[1] = T2 - (incl - zs);
+        }
+        if (l == 0) L.token = hs;
+    }
+    __syncthreads();
+    holder = L.token;  // every later write of these words follows a barrier
+    rem = L.uscratch[1];
+    MIS_STAMP(14);
+    return holder >= 0 ? 2 : 1;
 }
 
 __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
@@ -3829,180 +4128,6 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Row& R, in
     }
 }
 
-// The draw (engine/talker_sampler.py:161-172) from every slice's sub-block sums and the row's uniform u: the
-// sub-block that holds the target, then its 512 values in token order on one wave, weighed with the mass table.
-// Returns the token.
-__device__ __forceinline__ int64_t r2_draw(const DevGroup& G, const Row& R, Lds& L, float thr, float md, float x0,
-                                           float u) {
-    const int tid = threadIdx.x, l = lane_id();
-    const int nsb = kWaves * G.R, total = R.S * nsb;
-    const int per = (total + kThreads - 1) / kThreads;  // thread t: sums [t per, (t + 1) per) in (slice, sub-block) order
-    unsigned long long v[kMaxSlices * kMaxSB / kThreads + 1];
-    unsigned long long own = 0ull;
-#pragma unroll
-    for (int k = 0; k < kMaxSlices * kMaxSB / kThreads + 1; ++k) {
-        const int i = tid * per + k;
-        v[k] = 0ull;
-        if (k < per && i < total)
-            v[k] = pub_ld((const unsigned long long*)(rec_base(G, R.row, i / nsb) + kRecSbOff) + (i % nsb));
-        own += v[k];
-    }
-    unsigned long long zs;
-    if (tid == 0) L.token = -1;
-    const unsigned long long ex = block_excl_scan(own, zs, L.red.u);
-    const unsigned long long T2 = zs ? (unsigned long long)floor((double)u * (double)zs) + 1ull : 0ull;
-    if (own && ex < T2 && T2 <= ex + own) {
-        unsigned long long c = ex;
-#pragma unroll
-        for (int k = 0; k < kMaxSlices * kMaxSB / kThreads + 1; ++k) {
-            if (k >= per) break;
-            if (v[k] && c + v[k] >= T2) {
-                L.token = tid * per + k;
-                L.uscratch[1] = T2 - c;
-                break;
-            }
-            c += v[k];
-        }
-    }
-    __syncthreads();
-    const int hit = L.token;
-    MIS_STAMP(19);
-    if (hit < 0) return R.V - 1;  // no survivor mass (cannot happen with md finite)
-    const unsigned long long rem = L.uscratch[1];
-    const int s = hit / nsb, sbi = hit % nsb;
-    const int slo = s * G.slice_len, shi = min(R.V, slo + G.slice_len);
-    const Geo<2> g = slice_geo<2>(G, R.row, slo);
-    const int p0 = sbi * 512;  // positions [p0, p0 + 512) from g.first
-    // every load of the sub-block issued together: the slice's specials (all kSpecCap slots; the ones past nspec
-    // are dropped), and on wave 0 the logits and the mask words of lane l's 8 tokens
-    const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, s);
-    const unsigned long long* spl = (const unsigned long long*)((const char*)rec + kRecSpecOff);
-    constexpr int kSpecPer = kSpecCap / kThreads;
-    static_assert(kSpecPer * kThreads == kSpecCap, "specials per thread");
-    unsigned long long se[kSpecPer];
-    const int ns = min(pub_ld(&rec->nspec), kSpecCap);
-#pragma unroll
-    for (int q = 0; q < kSpecPer; ++q) se[q] = pub_ld(spl + q * kThreads + tid);
-    const int j0 = g.first + p0 + 8 * l;
-    const int ja = min(max(j0, slo), shi - 1), jb = min(max(j0 + 7, slo), shi - 1);
-    uint4 cv = make_uint4(0u, 0u, 0u, 0u);
-    uint32_t wa = ~0u, wb = ~0u;
-    if (wave_id() == 0) {
-        cv = load_chunk<2>(g, sbi * 64 + l, shi);
-        if (G.allowed) {
-            const auto aw = gp(G.allowed) + (int64_t)R.row * G.allowed_stride;
-            wa = aw[ja >> 5];
-            wb = aw[jb >> 5];
-        }
-    }
-    // the specials in the sub-block: their masses (or 0) and a mark that leaves them out of the logits, at
-    // [e][lane] for position 8 lane + e, so that wave 0 reads them without bank conflicts
-    unsigned long long* om = (unsigned long long*)&L.a;  // 512 masses
-    uint32_t* osp = (uint32_t*)(om + 512);                // 512 marks
-    if (tid < 512) {
-        om[tid] = 0ull;
-        osp[tid] = 0u;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < kSpecPer; ++q) {
-        const unsigned long long e = se[q];
-        const uint32_t id = (uint32_t)(e >> 32);
-        const int pos = (int)(id & ~kSelOnlyBit) - g.first - p0;
-        if (q * kThreads + tid < ns && pos >= 0 && pos < 512) {
-            const float qv = __uint_as_float((uint32_t)e);
-            const int at = (pos & 7) * 64 + (pos >> 3);
-            om[at] = (!(id & kSelOnlyBit) && qv >= thr) ? efx(qv, md) : 0ull;
-            osp[at] = 1u;
-        }
-    }
-    if (tid == 0 && R.eos_rule != kEosNormal && G.eos >= slo && G.eos < shi) {
-        const int pos = G.eos - g.first - p0;
-        if (pos >= 0 && pos < 512) osp[(pos & 7) * 64 + (pos >> 3)] = 1u;  // its mass stays 0
-    }
-    if (tid == 0) L.uscratch[0] = (unsigned long long)(R.V - 1);
-    __syncthreads();
-    MIS_STAMP(20);
-    if (wave_id() == 0) {
-        const unsigned long long* lut = lut_of(L);
-        const uint32_t wv[4] = {cv.x, cv.y, cv.z, cv.w};
-        unsigned long long m[8];
-        uint32_t bits = 0u;  // plain survivors: in the slice, allowed, not special, x >= x0
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int j = j0 + e;
-            const uint32_t w = (j >> 5) == (ja >> 5) ? wa : wb;
-            const bool sp = osp[e * 64 + l] != 0u;
-            m[e] = sp ? om[e * 64 + l] : 0ull;
-            const float x = __uint_as_float(((wv[e >> 1] >> (16 * (e & 1))) & 0xffffu) << 16);
-            if (!sp && j >= slo && j < shi && ((w >> (j & 31)) & 1u) && x >= x0) bits |= 1u << e;
-        }
-        uint32_t lumps = 0u;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            if (bits & (1u << e)) m[e] = r2_mass(lut, (wv[e >> 1] >> (16 * (e & 1))) & 0xffffu, e, lumps);
-        while (lumps) {  // rare: values within 2^-7 of zero
-            const int e = __ffs(lumps) - 1;
-            lumps &= lumps - 1u;
-            m[e] = efx(to_q<2>(R, __uint_as_float(((wv[e >> 1] >> (16 * (e & 1))) & 0xffffu) << 16)), md);
-        }
-        unsigned long long sum = 0ull;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sum += m[e];
-        const unsigned long long incl = wave_incl_scan(sum);
-        const unsigned long long exl = incl - sum;
-        const bool mine = sum && exl < rem && rem <= incl;
-        if (mine) {
-            unsigned long long c = exl;
-            int hitj = j0 + 7;
-            for (int e = 0; e < 8; ++e) {
-                if (m[e] && c + m[e] >= rem) {
-                    hitj = j0 + e;
-                    break;
-                }
-                c += m[e];
-            }
-            L.uscratch[0] = (unsigned long long)hitj;
-        }
-    }
-    __syncthreads();
-    return (int64_t)L.uscratch[0];
-}
-
-
-// The second round's last workgroup: the draw from the sub-block sums, then outputs and state; thr, md, x0 and u
-// are in L.fscratch.  A row some slice of which gave up waiting comes out as PAD, with its state untouched and the
-// workspace's error word raised.
-__device__ __forceinline__ void r2_finish(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L, bool failed) {
-    if (failed && threadIdx.x == 0) {  // this workgroup may have given up before the decision came
-        const float* dat = (const float*)(row_line(A, R) + kLineDat);
-        L.fscratch[0] = pub_ld(dat);
-        L.fscratch[1] = pub_ld(dat + 1);
-    }
-    __syncthreads();
-    Outcome o;
-    o.thr = L.fscratch[0];
-    o.mdraw = L.fscratch[1];
-    const float x0 = L.fscratch[2], u = L.fscratch[3];
-    __syncthreads();
-    MIS_STAMP(30);
-    o.token = failed ? (int64_t)kPad : r2_draw(G, R, L, o.thr, o.mdraw, x0, u);
-    MIS_STAMP(8);
-    if (threadIdx.x == 0 && G.paths) {
-        atomicAdd(G.paths + MIS_PATH_HISTOGRAM, 1u);
-        if (failed) atomicAdd(G.paths + (MIS_WS_ERROR_OFFSET - MIS_WS_PATH_OFFSET) / 4, 1u);
-    }
-    if (R.want_out) write_outputs(G, R, L, o, false);
-    if (failed) {
-        if (threadIdx.x == 0 && G.tokens) gp(G.tokens)[R.row] = kPad;
-        return;
-    }
-    update_state(G, R, o.token);
-    MIS_STAMP(10);
-    MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)R.slice << 8) | 0x80u |
-                   (unsigned)MIS_PATH_HISTOGRAM);
-}
-
 // The row's last workgroup (or slice 0 of a forced row).
 __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L, bool forced) {
     Outcome o;
@@ -4066,9 +4191,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const KernelArgs args)
     const DevGroup& G = A.g[gi];
     Row R;
     const int act = G.es == 2 ? run<2>(A, G, gi, row, slice, L, R) : run<4>(A, G, gi, row, slice, L, R);
-    if (act == kActR2Draw || act == kActR2Failed) {
-        r2_finish(A, G, R, L, act == kActR2Failed);
-    } else if (act != kActNone) {
+    if (act != kActNone) {
         if (act == kActForced) L.foreign = 0;
         if (act == kActStream) L.foreign = 1;  // finalised from the logits alone
         finalize(G, R, L, act == kActForced);

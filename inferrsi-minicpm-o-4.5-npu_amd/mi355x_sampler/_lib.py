@@ -22,6 +22,7 @@ MIS_HISTORY_WINDOW, MIS_HISTORY_RING = 0, 1
 MIS_TOPK_ZERO_DISABLES, MIS_TOPP_ONE_DISABLES, MIS_UPDATE_STATE, MIS_FINALIZE_STREAMING = 1, 2, 4, 8
 MIS_E_ARG, MIS_E_WORKSPACE, MIS_E_UNSUPPORTED = 1, 2, 3
 MIS_WS_PATH_OFFSET = 64
+MIS_WS_ERROR_OFFSET = 128  # u32: slices that gave up waiting for their row's finaliser (include/mi355x_sampler.h)
 MIS_STATIC_WORKSPACE_BYTES = 64 << 20
 PATHS = ("greedy", "full", "candidates", "histogram", "stream", "forced")  # MIS_PATH_* order
 
@@ -147,10 +148,21 @@ def path_counters(device: torch.device) -> dict[str, int]:
     return {p: int(v[i]) for i, p in enumerate(PATHS)}
 
 
+def wait_failures(device: torch.device) -> int:
+    """Slices that gave up waiting for their row's finaliser on the workspace of ``device``'s current stream since
+    the last reset (0 unless the device stalled a workgroup for milliseconds; synchronises)."""
+    buf = _ws.get(_ws_key(device))
+    if buf is None:
+        return 0
+    return int(buf[MIS_WS_ERROR_OFFSET:MIS_WS_ERROR_OFFSET + 4].view(torch.int32).item())
+
+
 def reset_path_counters(device: torch.device) -> None:
+    """Zeroes the path counters and the wait-failure count."""
     words = _path_words(device)
     if words is not None:
         words.zero_()
+        _ws[_ws_key(device)][MIS_WS_ERROR_OFFSET:MIS_WS_ERROR_OFFSET + 4].zero_()
 
 
 def sample(groups: list[MisGroup], device: torch.device) -> None:

@@ -138,6 +138,7 @@ def test_large_nucleus_second_pass(semantics):
                   prob_rtol=2e-3)
     # the wide rows are settled from the slices' value histograms, none by streaming the row
     assert paths["stream"] == 0 and paths["histogram"] >= 3 and sum(paths.values()) == rows
+    assert _lib.wait_failures(DEV) == 0
 
 
 def test_boundary_bin_and_candidate_rows_across_launches():
@@ -169,6 +170,46 @@ def test_boundary_bin_and_candidate_rows_across_launches():
                             min_new_tokens=2, semantics="hf", min_keep=3)
         compare_group(f"across_launches_{it}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows,
                       prob_rtol=2e-3)
+
+
+@pytest.mark.parametrize("case", ["tiny_values", "tiny_list_overflow", "one_slice"])
+def test_histogram_rows_with_values_at_zero(case):
+    """Top-p rows without top-k settled from value counts, with values crowding zero: exact +0 and -0, magnitudes
+    below 2^-15 (weighed one by one by the drawing slice), the slices' lists of tiny values overflowing (the row is
+    streamed instead), and a vocabulary of one slice (the finaliser draws itself)."""
+    print(f"[gpu] histogram rows at zero {case}", flush=True)
+    gen = torch.Generator().manual_seed(47)
+    rows = 6
+    v = 20000 if case == "one_slice" else W.THINKER_V
+    # six rows of the full vocabulary take 19 slices of 8,184 values: two thirds of them tiny overflow the lists
+    x = torch.randn(rows, v, generator=gen) * (0.008 if case == "tiny_list_overflow" else 0.3)
+    x[torch.rand(rows, v, generator=gen) < 0.01] = 0.0
+    x[:, 1::997] = -0.0
+    x[:, 3::1009] = 1e-6
+    x[:, 5::1013] = -2e-6
+    x = x.to(torch.bfloat16)
+    hist = torch.randint(0, v, (rows, 256), generator=gen, dtype=torch.int64).to(torch.int32)
+    one = lambda val, dt=torch.float32: torch.full((rows,), val, dtype=dt)  # noqa: E731
+    temps = torch.tensor([0.05, 0.1, 0.3, 1.0, 0.02, 0.5])
+    top_p = torch.tensor([0.9, 0.5, 0.95, 0.8, 0.7, 0.99])
+    ref_rows = ext.Rows(logits=x, temperature=temps, top_k=one(0, torch.int32), top_p=top_p, repetition=one(1.1),
+                        presence=one(0.0), frequency=one(0.0), history=hist, seeds=one(7, torch.int64),
+                        steps=one(2, torch.int64))
+    g = G.RowGroup(x.to(DEV), temperature=temps.to(DEV), top_k=0, top_p=top_p.to(DEV), repetition=1.1,
+                   history=hist.to(DEV), seeds=one(7, torch.int64).to(DEV), steps=one(2, torch.int64).to(DEV),
+                   processed=True, probs=True)
+    _lib.reset_path_counters(DEV)
+    G.launch([g])
+    torch.cuda.synchronize()
+    paths = _lib.path_counters(DEV)
+    print(f"[gpu] histogram rows at zero {case} paths {paths}", flush=True)
+    compare_group(f"at_zero_{case}", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows,
+                  prob_rtol=2e-3)
+    assert _lib.wait_failures(DEV) == 0
+    if case == "tiny_list_overflow":
+        assert paths["stream"] == rows
+    else:
+        assert paths["histogram"] == rows and paths["stream"] == 0
 
 
 def test_thinker_greedy_is_first_argmax_at_full_size():
