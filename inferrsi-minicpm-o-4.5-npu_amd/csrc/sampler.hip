@@ -762,6 +762,24 @@ __device__ __forceinline__ int bf_key(uint32_t b) {
     return neg ? kKeyZero - 2 - m : kKeyZero + 2 + m;
 }
 
+// bf_key of the two bf16 values of word v (low half: the lower element), in 16-bit lanes; in tiny their magnitude
+// patterns minus one (below kBfLo - 1 exactly for a magnitude in (0, 2^-7)).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t hist_key2(uint32_t v, uint32_t& tiny) {
+    const u16x2 w = __builtin_bit_cast(u16x2, v);
+    const u16x2 sg = __builtin_bit_cast(u16x2, __builtin_bit_cast(i16x2, v) >> (i16x2)15);  // 0xffff: negative
+    const u16x2 a = w & (u16x2)0x7fff;
+    u16x2 m = __builtin_elementwise_max(a, (u16x2)(kBfLo - 1));
+    m = __builtin_elementwise_min(m, (u16x2)kBfHi) - (u16x2)(kBfLo - 1);  // 0 below 2^-7, 0x781 from 256 up
+    const u16x2 u = __builtin_elementwise_min(a, (u16x2)1) + m;            // 0 for zero, 1 for the tiny lump
+    tiny = __builtin_bit_cast(uint32_t, a - (u16x2)1);
+    return __builtin_bit_cast(uint32_t, ((u ^ sg) - sg) + (u16x2)kKeyZero);
+}
+
+// A tile value the histogram counts: not the -inf of a masked element, not NaN.
+__device__ __forceinline__ bool hist_counted(uint32_t b) { return b != 0xff80u && (b & 0x7fffu) <= 0x7f80u; }
+
 // Keys that hold one value: every key but the lumps (0, kKeyZero - 1, kKeyZero + 1, kKeys - 1).
 __device__ __forceinline__ bool key_exact(int k) {
     return k >= 1 && k <= kKeys - 2 && k != kKeyZero - 1 && k != kKeyZero + 1;
@@ -866,9 +884,6 @@ static_assert(kTabMarkOff + 8 * 12 <= kChunkOff && kChunkOff + 8 * kWaves * kRou
 constexpr int kStageOff = 65536;
 static_assert(16 * (kKeys + 1) + 12 * 256 <= kStageOff && kStageOff + 16 * kHistWords <= (int)sizeof(Lds::a),
               "the histogram finaliser's tables and staged counts");
-
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
-typedef short i16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ char* row_line(const KernelArgs& A, const Row& R) {
     return A.arrive + (int64_t)R.grow * kLineBytes;
@@ -1404,18 +1419,18 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
 
     if constexpr (ES == 2) {
         if (nucleus_hist(R, ES)) {
-            // the count of every value at or above a value gate (the nucleus histogram), and the summed mass of the
-            // values below it: the values below mq - D weigh at most V e^-D of the row's largest, less than the
-            // 1 - top_p of the row the cut leaves below it, so the cut lies above them whenever the row's largest
-            // is in the slice; the finaliser checks that its cut lies above every slice's bound hb and streams the
-            // row otherwise
+            // the count of every value of the tile (the nucleus histogram), and for the specials a value gate: the
+            // specials below mq - D weigh at most V e^-D of the row's largest, less than the 1 - top_p of the row the
+            // cut leaves below it, so the cut lies above them whenever the row's largest is in the slice; they are
+            // summed (z), and the finaliser checks that its cut lies above every slice's gate and streams the row
+            // otherwise
             const float D = R.top_p < 1.0f ? __logf((float)R.V) - log1pf(-R.top_p) + 2.0f : INFINITY;
             const float gate_q = mq - D;
-            const float g_raw = gate_q * R.T;  // tile domain: x >= g_raw is counted
-            const float hb = fmaxf(to_q<2>(R, g_raw), gate_q);  // every value left out is <= hb
+            const float hb = gate_q;  // every value left out is a special below it
             // kHistReps copies of the counts (lane l adds to copy l % kHistReps, so lanes of a wave that hold one
             // value spread their LDS atomics over several addresses and banks; the history counts are no longer
-            // needed); the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0)
+            // needed); the tiny-magnitude lumps also carry their sum of exp(q) (q within 2^-7 / T of 0), and their
+            // values are listed
             uint4* hk4 = (uint4*)L.a.cnt;
             for (int i = tid; i < kHistReps * kHistStride / 4; i += kThreads) hk4[i] = make_uint4(0u, 0u, 0u, 0u);
             if (tid == 0) {
@@ -1429,30 +1444,35 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
             uint32_t* lumps = (uint32_t*)((char*)rec + kRecLumpOff);
             unsigned long long tf = 0ull;
-            // sum of exp(q - mq) over what is left out, as 2^(x log2(e) / T - mq log2(e)) in float: these masses
-            // sum to at most V e^-D of the row's largest, so their relative error of a few 1e-6 stays far below
-            // the counts' fixed-point resolution of the total
-            const float c1 = (float)(1.4426950408889634 / (double)R.T), c2 = mq * 1.44269502f;
             float zr = 0.0f;
 #pragma unroll
             for (int r = 0; r < RMAX; ++r) {
                 if (r >= RR) continue;
                 const uint32_t wv[4] = {t[r].x, t[r].y, t[r].z, t[r].w};
+                uint32_t tmin = 0xffffffffu;
 #pragma unroll
-                for (int h = 0; h < 8; ++h) {
-                    const uint32_t b = (wv[h >> 1] >> (16 * (h & 1))) & 0xffffu;
-                    const float x = __uint_as_float(b << 16);
-                    if (b == 0xff80u) continue;
-                    if (x >= g_raw) {
-                        const int k = bf_key(b);
-                        atomicAdd(&hk[k], 1u);
-                        if (k == kKeyZero - 1 || k == kKeyZero + 1) {
-                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, x)) * kFx);
+                for (int h = 0; h < 4; ++h) {
+                    uint32_t tn;
+                    const uint32_t k2 = hist_key2(wv[h], tn);
+                    tmin = __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, tmin),
+                                                                                   __builtin_bit_cast(u16x2, tn)));
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const uint32_t b = (wv[h] >> (16 * e)) & 0xffffu;
+                        if (hist_counted(b)) atomicAdd(&hk[(k2 >> (16 * e)) & 0xffffu], 1u);
+                    }
+                }
+                if (ballot((tmin & 0xffffu) < kBfLo - 1u || (tmin >> 16) < kBfLo - 1u)) {
+                    // rare: magnitudes in (0, 2^-7), the lumps next to zero
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t b = (wv[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+                        const uint32_t a = b & 0x7fffu;
+                        if (a != 0u && a < kBfLo) {
+                            tf += (unsigned long long)((double)exp_acc(to_q<2>(R, __uint_as_float(b << 16))) * kFx);
                             const int slot = atomicAdd(&L.nlump, 1);
                             if (slot < kLumpCap) lumps[slot] = b;
                         }
-                    } else if (x == x) {
-                        zr += __builtin_amdgcn_exp2f(__builtin_fmaf(x, c1, -c2));
                     }
                 }
             }
