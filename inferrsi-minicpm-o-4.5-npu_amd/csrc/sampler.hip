@@ -808,19 +808,23 @@ __device__ __forceinline__ float key_q(const Row& R, int k) {
 // strictly between that value and the next key's; -1 below every key.  qt(k) is key_q(R, k) (computed or from a
 // table).  engine/talker_sampler.py:87-92 ranks values, so equal values share a bin.
 template <class QT>
-__device__ __forceinline__ int hist_bin(const Row& R, float q, QT&& qt) {
-    if (!(q >= qt(1))) return -1;
+__device__ __forceinline__ int hist_bin(const Row& R, float q, float q1, QT&& qt) {
+    if (!(q >= q1)) return -1;  // q1 = qt(1)
     // the largest key whose value is <= q: the bf16 value nearest q T is within a key or two of it (q is x / T
-    // rounded once for the bf16 x of an exact key, and a special lies between two such values)
+    // rounded once for the bf16 x of an exact key, and a special lies between two such values); its value and the
+    // next key's are taken once, and a step away from the guess takes one more
     const uint32_t yb = __float_as_uint(q * R.T);
     int lo = min(max(bf_key((yb + 0x7fffu + ((yb >> 16) & 1u)) >> 16), 1), kKeys - 1);
-    for (int it = 0; it < 4; ++it) {
-        if (qt(lo) > q)
-            --lo;
-        else if (lo + 1 < kKeys && qt(lo + 1) <= q)
-            ++lo;
+    float qlo = qt(lo);
+    int it = 0;
+    for (; qlo > q && lo > 1 && it < 4; ++it) qlo = qt(--lo);
+    float qhi = lo + 1 < kKeys ? qt(lo + 1) : INFINITY;
+    for (; qhi <= q && it < 8; ++it) {
+        ++lo;
+        qlo = qhi;
+        qhi = lo + 1 < kKeys ? qt(lo + 1) : INFINITY;
     }
-    if (!(qt(lo) <= q && (lo + 1 >= kKeys || q < qt(lo + 1)))) {
+    if (!(qlo <= q && q < qhi)) {
         lo = 1;
         int hi = kKeys;  // qt(lo) <= q < qt(hi)
         while (hi - lo > 1) {
@@ -830,9 +834,11 @@ __device__ __forceinline__ int hist_bin(const Row& R, float q, QT&& qt) {
             else
                 hi = mid;
         }
+        qlo = qt(lo);
     }
+    // a lump takes the value of the exact key below it, so qt(k) is qlo either way
     const int k = key_exact(lo) ? lo : lo - 1;
-    return qt(k) == q ? 2 * k : 2 * k + 1;
+    return qlo == q ? 2 * k : 2 * k + 1;
 }
 
 // Top-p rows without top-k on bf16 logits are settled from value counts (the histogram path).
@@ -1483,6 +1489,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             // the ones below the gate are listed only for the draw's pass over the slice)
             unsigned long long* sg = (unsigned long long*)((char*)rec + kRecSpecOff);
             uint32_t* sbin = (uint32_t*)((char*)rec + kRecSpecBinOff);
+            const float q1 = key_q(R, 1);
             for (int i0 = 0; i0 < ns; i0 += kThreads) {
                 const int i = i0 + tid;
                 const float q = i < ns ? L.spec[i].q : -INFINITY;
@@ -1494,7 +1501,8 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                     const int slot = high ? sh : ns - 1 - sl;
                     sg[slot] = ((unsigned long long)((uint32_t)L.spec[i].j | (L.spec[i].sel ? kSelOnlyBit : 0u)) << 32) |
                                __float_as_uint(q);
-                    const int b = high ? hist_bin(R, q, [&](int k) { return key_q(R, k); }) : -1;
+                    int b = -1;
+                    if (high) b = hist_bin(R, q, q1, [&](int k) { return key_q(R, k); });
                     sbin[slot] = (uint32_t)(b + 1);  // 0: below every key or -inf
                     if (low && q > -INFINITY) zr += exp_acc(q - mq);
                 }
