@@ -161,16 +161,12 @@ struct SliceRec {
     int32_t ncand[kSegs];
     int32_t nhigh;   // histogram path: the first nhigh published specials lie at or above the value gate
     unsigned long long tinyfx;  // sum of exp(q) in fixed point over the tiny-magnitude lumps of the histogram
-    int32_t nlump;              // histogram path: the tiny-magnitude values listed (bf16 patterns)
+    unsigned long long zsurv;   // histogram path: the slice's survivor mass for the draw (after the cut)
 };
 constexpr int64_t kRecHead = 256;
 static_assert(sizeof(SliceRec) <= kRecHead, "slice record");
 constexpr int64_t kRecSbOff = kRecHead;
 constexpr int64_t kRecCandOff = kRecSbOff + 8 * kMaxSB;
-// Histogram slices publish no candidates: the candidate area holds the bf16 patterns of their tiny-magnitude values
-// (the lumps next to zero) instead, for the draw's exact survivor mass.
-constexpr int64_t kRecLumpOff = kRecCandOff;
-constexpr int kLumpCap = 4096;
 // Nucleus histogram of a bf16 slice: one key per bf16 value with |x| in [2^-7, 2^8) (1,920 per sign), zero, the
 // tiny magnitudes of each sign (lumps) and the huge ones (lumps); keys increase with the value.
 constexpr int kKeys = 3845;
@@ -250,7 +246,6 @@ struct Lds {
     int32_t flags;
     int32_t is_last;
     int32_t nhi, nlo;  // slice phase of the histogram path: specials at or above the value gate, and below it
-    int32_t nlump;     // slice phase of the histogram path: tiny-magnitude values listed
     int32_t foreign;
     int32_t token;
     float fscratch[4];
@@ -852,25 +847,24 @@ __device__ __forceinline__ void update_state(const DevGroup& G, const Row& R, in
 
 // ------------------------------------------------------------------ the histogram path's draw
 //
-// After a top-p row's cut is settled from the value counts, the finaliser also has every slice's exact survivor mass
-// (its counts weighed by value, its listed tiny values, its drawable specials: the same integers the slice's own
-// elements sum to), so it knows which slice holds the draw's target and where the target lies in that slice's
-// survivor mass.  The row's other slices keep their tiles in registers and wait on the row's line; the finaliser
-// first publishes the draw's reference md (the row's largest drawable value), so that they build the table of masses
-// by value while it settles the cut, then the decision.  The slice that holds the target sums its 512-value
-// sub-blocks and draws inside one of them from its registers; the others leave.  A waiting slice waits only for
-// its row's finaliser, which has arrived and is running, so the wait ends whatever the scheduling; a slice that
-// still gives up (after kR2SpinTicks) raises the workspace's error word, and when it held the target the row comes
-// out as PAD (written by the finaliser before the decision) with its state untouched.
+// After a top-p row's cut is settled from the value counts, the draw needs every slice's survivor mass, in token
+// order.  The row's slices other than the finaliser keep their tiles in registers and wait on the row's line.  The
+// finaliser first publishes the draw's reference md (the row's largest drawable value), so that they build the table
+// of masses by value while it settles the cut; then the cut, md, x0 and the row's uniform.  Every slice then sums its
+// survivors chunk by chunk (in LDS), publishes its total, and waits until all of the row's totals are out; the slice
+// that holds the target then walks wave, chunk and value from its registers; the others leave.  A waiting slice waits
+// only for slices of its row that have arrived and are running, so every wait ends whatever the scheduling; a slice
+// that still gives up (after kR2SpinTicks) counts itself in with a failure mark and raises the workspace's error
+// word; the row then comes out as PAD (written by the finaliser before its decision) with its state untouched.
 
 constexpr int kLineDec = 64;   // u32 on the row's line: 0 pending, 3 md published, 1 settled by the finaliser (the
-                               // row is streamed), 2 drawn by the holder
-constexpr int kLineSeen = 68;  // u32: slices done with the line (the finaliser after its decision)
-constexpr int kLineDat = 72;   // f32 thr, md, x0 (the least bf16 value x with x / T >= thr)
-constexpr int kLineHolder = 84;  // u32: the slice that holds the target
-constexpr int kLineRem = 88;     // u64: the target within the holder's survivor mass (1-based)
+                               // row is streamed), 2 cut published: every slice sums its survivors
+constexpr int kLineSeen = 68;  // u32: slices done with the line (the last clears it)
+constexpr int kLineDat = 72;   // f32 thr, md, x0 (the least bf16 value x with x / T >= thr), u (the row's uniform)
+constexpr int kLineSums = 88;  // u32: slices whose survivor mass is published (low 16 bits), failures (high 16 bits)
 constexpr unsigned long long kR2SpinTicks = 200000ull;  // 2 ms of the 100 MHz real-time counter
-static_assert(kLineRem + 8 <= kLineBytes, "row line");
+static_assert(kLineSums + 4 <= kLineBytes, "row line");
+
 
 // The holder's table of masses by bf16 value: entry kTabB + m for x >= 0 and kTabB - m for x < 0, where m = 0 for
 // |x| < 2^-15 (the entry holds zero's mass; the other values there are weighed one by one), m = 1 + a - kTabLo for
@@ -885,11 +879,7 @@ constexpr int kTabMarkOff = 8 * (kTabSize + 1);     // the draw's chunk marks fo
 constexpr int kChunkOff = 49152;                    // then the holder's chunk masses, [wave][round][lane]
 static_assert(kTabMarkOff + 8 * 12 <= kChunkOff && kChunkOff + 8 * kWaves * kRounds * 64 <= (int)sizeof(Lds::a),
               "mass table");
-// The histogram finaliser keeps the first four slices' counts here (past its own tables, below 64 KB) for the
-// draw's survivor masses.
-constexpr int kStageOff = 65536;
-static_assert(16 * (kKeys + 1) + 12 * 256 <= kStageOff && kStageOff + 16 * kHistWords <= (int)sizeof(Lds::a),
-              "the histogram finaliser's tables and staged counts");
+static_assert(16 * (kKeys + 1) + 12 * 256 <= (int)sizeof(Lds::a), "the histogram finaliser's tables");
 
 __device__ __forceinline__ char* row_line(const KernelArgs& A, const Row& R) {
     return A.arrive + (int64_t)R.grow * kLineBytes;
@@ -944,17 +934,16 @@ __device__ __forceinline__ void r2_tab_cut(Lds& L, float x0) {
     }
 }
 
-// The finaliser's words (thread 0): dec 3 with md, then 1, or 2 with thr, md, x0, the holder and the target.
+// The finaliser's words (thread 0): dec 3 with md, then 1, or 2 with thr, md, x0 and u.
 __device__ __forceinline__ void r2_decide(const KernelArgs& A, const Row& R, unsigned dec, float thr, float md, float x0,
-                                          int holder, unsigned long long rem) {
+                                          float u) {
     if (threadIdx.x != 0) return;
     char* line = row_line(A, R);
     float* d = (float*)(line + kLineDat);
     if (dec == 2u) {
         d[0] = thr;
         d[2] = x0;
-        *(uint32_t*)(line + kLineHolder) = (uint32_t)holder;
-        *(unsigned long long*)(line + kLineRem) = rem;
+        d[3] = u;
     }
     if (dec != 1u) d[1] = md;
     wait_stores();
@@ -970,13 +959,14 @@ __device__ __forceinline__ void r2_seen(const KernelArgs& A, const DevGroup& G, 
     const unsigned now = __hip_atomic_fetch_add(sw, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     if ((int)now == R.S) {
         __hip_atomic_store((unsigned*)(line + kLineDec), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store((unsigned*)(line + kLineSums), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(sw, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (gave_up && G.paths) atomicAdd(G.paths + (MIS_WS_ERROR_OFFSET - MIS_WS_PATH_OFFSET) / 4, 1u);
 }
 
-// A waiting slice: the decision (0 if it gave up waiting).  With 2, L.fscratch holds thr, md, x0, L.scnt the holder
-// and L.uscratch[0] the target; the table is built on the way (without its bound x0), as soon as md is out.
+// A waiting slice: the decision (0 if it gave up waiting).  With 2, L.fscratch holds thr, md, x0, u; the table is
+// built on the way (without its bound x0), as soon as md is out.
 __device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, Lds& L) {
     const char* line = row_line(A, R);
     unsigned* dw = (unsigned*)(line + kLineDec);
@@ -997,8 +987,7 @@ __device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, L
             if (d == 2u) {
                 L.fscratch[0] = pub_ld(dat);
                 L.fscratch[2] = pub_ld(dat + 2);
-                L.scnt = (int)pub_ld((const uint32_t*)(line + kLineHolder));
-                L.uscratch[0] = pub_ld((const unsigned long long*)(line + kLineRem));
+                L.fscratch[3] = pub_ld(dat + 3);
             }
             if (d >= 2u) L.fscratch[1] = pub_ld(dat + 1);
             L.token = (int)d;
@@ -1013,6 +1002,54 @@ __device__ __forceinline__ unsigned r2_wait(const KernelArgs& A, const Row& R, L
         __syncthreads();  // the table complete, and L.token read by every thread before thread 0 writes it again
         if (d == 2u) return d;
     }
+}
+
+// The survivor-mass exchange (every thread): this slice's total z (or a failure mark) goes to its record and the
+// row's count; once all of the row's totals are out, the slice that holds the target floor(u Z) + 1 of the total Z
+// and the target within it (L.token, L.uscratch[0]).  -1: no draw here (no mass, a failure, or a slice that gave
+// up waiting).
+__device__ __forceinline__ int r2_exchange(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
+                                           unsigned long long z, bool failed, float u) {
+    const int tid = threadIdx.x, l = lane_id();
+    char* line = row_line(A, R);
+    unsigned* cw = (unsigned*)(line + kLineSums);
+    if (tid == 0) {
+        ((SliceRec*)rec_base(G, R.row, R.slice))->zsurv = z;
+        wait_stores();
+        __hip_atomic_fetch_add(cw, failed ? 0x10001u : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        unsigned c = __hip_atomic_load(cw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool gave_up = false;
+        while ((int)(c & 0xffffu) < R.S) {
+            if (__builtin_amdgcn_s_memrealtime() - t0 > kR2SpinTicks) {
+                gave_up = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            c = __hip_atomic_load(cw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        L.flags = (gave_up || (c >> 16) != 0u) ? 1 : 0;
+        r2_seen(A, G, R, gave_up);
+        L.token = -1;
+    }
+    __syncthreads();
+    if (L.flags) return -1;
+    if (wave_id() == 0) {
+        const unsigned long long zs = l < R.S ? pub_ld(&((const SliceRec*)rec_base(G, R.row, l))->zsurv) : 0ull;
+        const unsigned long long incl = wave_incl_scan(zs);
+        const unsigned long long Z = readlane_u64(incl, 63);
+        if (Z) {
+            const double pt = floor((double)u * (double)Z) + 1.0;
+            const unsigned long long T2 = pt >= (double)Z ? Z : (unsigned long long)pt;
+            const uint64_t h = ballot(incl >= T2);
+            if (l == __ffsll((long long)h) - 1) {
+                L.token = l;
+                L.uscratch[0] = T2 - (incl - zs);
+            }
+        }
+    }
+    __syncthreads();
+    return L.token;
 }
 
 // The least bf16 value x with x / T >= thr (finite thr), the same in every lane of the calling wave: x0 lies within
@@ -1067,12 +1104,11 @@ __device__ __forceinline__ void r2_chunk_masses(const Row& R, const unsigned lon
     }
 }
 
-// The holder's draw.  Each lane's survivor mass per round (the 8 values of one 16-byte chunk) goes to LDS and the
-// wave's total to one reduction; each drawable special's mass is added to its chunk and its wave.  Wave 0 then
-// finds the wave that holds the target, that wave the chunk (a scan over its lanes, round by round: chunks are in
-// token order), and the chunk's lane the token.  The table must be built with its bound.
-__device__ __forceinline__ int64_t r2_hold(const Row& R, Lds& L, const uint4 (&t)[kRounds], int RR, int first, int ns,
-                                           float thr, float md, float x0, unsigned long long rem) {
+// A slice's survivor mass.  Each lane's survivor mass per round (the 8 values of one 16-byte chunk) goes to LDS and
+// the wave's total to one reduction; each drawable special's mass is added to its chunk and its wave.  Returns the
+// slice's total.  The table must be built with its bound.
+__device__ __forceinline__ unsigned long long r2_chunks(const Row& R, Lds& L, const uint4 (&t)[kRounds], int RR,
+                                                        int first, int ns, float thr, float md, float x0) {
     const int tid = threadIdx.x, w = wave_id(), l = lane_id();
     const unsigned long long* tab = tab_of(L);
     unsigned long long* cs = (unsigned long long*)((char*)&L.a + kChunkOff);  // [wave][round][lane]
@@ -1107,9 +1143,25 @@ __device__ __forceinline__ int64_t r2_hold(const Row& R, Lds& L, const uint4 (&t
             atomicAdd(&L.sbfx[sw], f);
         }
     }
-    if (tid == 0) L.scnt = -1;
     __syncthreads();
     MIS_STAMP(18);
+    unsigned long long z = 0ull;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) z += L.sbfx[i];
+    return z;
+}
+
+// The holder's walk: the wave that holds the target rem (1-based, within the slice's survivor mass), that wave's
+// chunk (a scan over its lanes, round by round: chunks are in token order), then the chunk's value.  L keeps what
+// r2_chunks left.
+__device__ __forceinline__ int64_t r2_walk(const Row& R, Lds& L, const uint4 (&t)[kRounds], int RR, int first, int ns,
+                                           float thr, float md, float x0, unsigned long long rem) {
+    const int tid = threadIdx.x, w = wave_id(), l = lane_id();
+    const unsigned long long* tab = tab_of(L);
+    unsigned long long* cs = (unsigned long long*)((char*)&L.a + kChunkOff);
+    const uint32_t* smark = L.keep;
+    if (tid == 0) L.scnt = -1;
+    __syncthreads();
     // the wave of the target (every wave finds it), then that wave's chunk, round by round
     int hw;
     unsigned long long rw;
@@ -1191,7 +1243,7 @@ __device__ __forceinline__ int64_t r2_hold(const Row& R, Lds& L, const uint4 (&t
 }
 
 __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
-                                        Outcome& out, float& x0, int& holder, unsigned long long& rem);
+                                        Outcome& out);
 
 enum : int { kActNone = 0, kActFinalize = 1, kActForced = 2, kActStream = 3 };
 
@@ -1443,12 +1495,10 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 L.tinyfx = 0ull;
                 L.nhi = 0;
                 L.nlo = 0;
-                L.nlump = 0;
             }
             __syncthreads();
             MIS_STAMP(26);
             uint32_t* hk = L.a.cnt + (l % kHistReps) * kHistStride;
-            uint32_t* lumps = (uint32_t*)((char*)rec + kRecLumpOff);
             unsigned long long tf = 0ull;
             float zr = 0.0f;
 #pragma unroll
@@ -1474,11 +1524,8 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                     for (int e = 0; e < 8; ++e) {
                         const uint32_t b = (wv[e >> 1] >> (16 * (e & 1))) & 0xffffu;
                         const uint32_t a = b & 0x7fffu;
-                        if (a != 0u && a < kBfLo) {
+                        if (a != 0u && a < kBfLo)
                             tf += (unsigned long long)((double)exp_acc(to_q<2>(R, __uint_as_float(b << 16))) * kFx);
-                            const int slot = atomicAdd(&L.nlump, 1);
-                            if (slot < kLumpCap) lumps[slot] = b;
-                        }
                     }
                 }
             }
@@ -1531,64 +1578,80 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
                 rec->gate = hb;
                 rec->mref = mq;
                 rec->z = z;
-                rec->flags = L.flags | (L.nlump > kLumpCap ? kRecOverflow : 0);
+                rec->flags = L.flags;
                 rec->hist = 1;
                 rec->nspec = ns;
                 rec->nhigh = L.nhi;
                 rec->tinyfx = L.tinyfx;
-                rec->nlump = min(L.nlump, kLumpCap);
             }
             Outcome o;
-            float x0 = 0.f;
-            unsigned long long rem = 0ull;
+            float x0 = 0.f, u = 0.f;
             const bool fin = arrive(A, R, L);
             if (!fin) {
-                // held, the tile in registers, until the finaliser's decision; the slice that holds the draw's
-                // target draws it
+                // held, the tile in registers, until the finaliser's cut
                 const unsigned d = r2_wait(A, R, L);
                 MIS_STAMP(9);
-                if (d != 2u || L.scnt != R.slice) {
-                    r2_seen(A, G, R, d == 0u);
+                if (d == 1u) {
+                    r2_seen(A, G, R, false);
+                    return kActNone;
+                }
+                if (d == 0u) {  // gave up: counted in with a failure mark, so that no slice waits for its total
+                    if (tid == 0) {
+                        __hip_atomic_fetch_add((unsigned*)(row_line(A, R) + kLineSums), 0x10001u, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+                        r2_seen(A, G, R, true);
+                    }
                     return kActNone;
                 }
                 o.thr = L.fscratch[0];
                 o.mdraw = L.fscratch[1];
                 x0 = L.fscratch[2];
-                rem = L.uscratch[0];
+                u = L.fscratch[3];
                 r2_tab_cut(L, x0);
             } else {
-                // the row's finaliser, its tile still in registers: the cut and the target's slice from every
-                // slice's counts
-                int holder = -1;
-                const int res = L.foreign ? 0 : fin_hist(A, G, R, L, o, x0, holder, rem);
+                // the row's finaliser, its tile still in registers: the cut from every slice's counts
+                const int res = L.foreign ? 0 : fin_hist(A, G, R, L, o);
                 MIS_STAMP(9);
                 if (res != 2) {  // the row is streamed: the waiting slices are released
                     if (R.S > 1) {
-                        r2_decide(A, R, 1u, 0.f, 0.f, 0.f, 0, 0ull);
+                        r2_decide(A, R, 1u, 0.f, 0.f, 0.f, 0.f);
                         r2_seen(A, G, R, false);
                     }
                     return kActStream;
                 }
+                x0 = r2_x0(R, o.thr);
+                u = L.fscratch[3];
                 if (R.S > 1) {
-                    if (holder != R.slice && tid == 0 && G.tokens) gp(G.tokens)[R.row] = kPad;  // the holder's later
-                    r2_decide(A, R, 2u, o.thr, o.mdraw, x0, holder, rem);
+                    if (tid == 0 && G.tokens) gp(G.tokens)[R.row] = kPad;  // until the holder writes the token
+                    r2_decide(A, R, 2u, o.thr, o.mdraw, x0, u);
                 }
                 if (tid == 0 && G.paths) atomicAdd(G.paths + MIS_PATH_HISTOGRAM, 1u);
-                if (holder != R.slice) {
-                    if (R.want_out) write_outputs(G, R, L, o, false);
-                    if (R.S > 1) r2_seen(A, G, R, false);
-                    return kActNone;
-                }
                 r2_tab(R, L, o.mdraw, x0);
             }
             __syncthreads();
-            o.token = r2_hold(R, L, t, RR, geo.first, ns, o.thr, o.mdraw, x0, rem);
+            MIS_STAMP(14);
+            // every slice: its survivor mass; then the slice that holds the target walks to it
+            const unsigned long long z = r2_chunks(R, L, t, RR, geo.first, ns, o.thr, o.mdraw, x0);
+            int holder = 0;
+            unsigned long long rem = 0ull;
+            if (R.S > 1) {
+                holder = r2_exchange(A, G, R, L, z, false, u);
+                rem = L.uscratch[0];
+            } else if (z) {
+                const double pt = floor((double)u * (double)z) + 1.0;
+                rem = pt >= (double)z ? z : (unsigned long long)pt;
+            } else {
+                holder = -1;
+            }
+            MIS_STAMP(15);
+            if (holder == R.slice) {
+                o.token = r2_walk(R, L, t, RR, geo.first, ns, o.thr, o.mdraw, x0, rem);
+                update_state(G, R, o.token);
+                MIS_STAMP(10);
+                MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)R.slice << 8) | 0x80u |
+                               (unsigned)MIS_PATH_HISTOGRAM);
+            }
             if (fin && R.want_out) write_outputs(G, R, L, o, false);
-            update_state(G, R, o.token);
-            if (R.S > 1) r2_seen(A, G, R, false);  // after the draw: its wait is off the path
-            MIS_STAMP(10);
-            MIS_STAMP_INFO(((unsigned long long)(R.grow + 1) << 32) | ((unsigned long long)R.slice << 8) | 0x80u |
-                           (unsigned)MIS_PATH_HISTOGRAM);
             return kActNone;
         }
     }
@@ -3555,8 +3618,8 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
 // falls).  Each slice's survivor mass follows from its counts; the draw streams the one slice that holds it.
 // False: the row is streamed instead.
 // 0: the row must be streamed; 1: no survivor; 2: the cut (out.thr, out.mdraw) for the second round.
-__device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L, Outcome& out,
-                                        float& x0, int& holder, unsigned long long& rem) {
+__device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
+                                        Outcome& out) {
     const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
     if (tid == 0) L.fscratch[3] = row_uniform(G, R);  // the draw's
     if (w == 0) {  // lane s reads slice s's record
@@ -3608,9 +3671,8 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
     out.mdraw = -INFINITY;
     out.token = R.V - 1;
     if (!(m > -INFINITY)) return 1;
-    const float u = L.fscratch[3];
     // md to the waiting slices, which build their mass tables while the cut is settled here
-    if (S > 1 && mdraw > -INFINITY) r2_decide(A, R, 3u, 0.f, mdraw, 0.f, 0, 0ull);
+    if (S > 1 && mdraw > -INFINITY) r2_decide(A, R, 3u, 0.f, mdraw, 0.f, 0.f);
     // every slice's counts, merged: the first four slices' loads are in flight while the mass table is built
     uint32_t* cnt = (uint32_t*)L.h.w;
     constexpr int kMI = (kHistWords + kThreads - 1) / kThreads;
@@ -3624,8 +3686,6 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
                              ? pub_ld((const uint32_t*)(rec_base(G, R.row, u4) + kRecHistOff) + i)
                              : 0u;
     }
-    // the first four slices' counts also stay in LDS, for the draw's survivor masses
-    uint32_t* stc = (uint32_t*)((char*)&L.a + kStageOff);
 #pragma unroll
     for (int mi = 0; mi < kMI; ++mi) {
         const int i = mi * kThreads + tid;
@@ -3634,7 +3694,6 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
         for (int u4 = 0; u4 < 4; ++u4) {
             a += hv[mi][u4] & 0xffffu;
             b += hv[mi][u4] >> 16;
-            if (i < kHistWords) stc[u4 * kHistWords + i] = hv[mi][u4];
         }
         for (int s0 = 4; s0 < S; s0 += 4) {
             uint32_t v[4];
@@ -3852,147 +3911,8 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
     const float md = mdraw >= thr ? mdraw : -INFINITY;
     out.thr = thr;
     out.mdraw = md;
-    if (!(md > -INFINITY)) return 1;
     MIS_STAMP(13);
-    // the draw's target: every slice's survivor mass (its counted values by key, its listed tiny values, its
-    // drawable specials: the integers its own elements sum to), then the slice that holds the target and the target
-    // within that slice's mass
-    x0 = r2_x0(R, thr);
-    const int k0 = bf_key(__float_as_uint(x0) >> 16);
-    if (k0 == 0 && cnt[0] != 0u) return 0;  // values of -256 and below may survive: not resolved here
-    MIS_STAMP(15);
-    if (tid < kMaxSlices) L.slice_u[tid] = 0ull;
-    // the loads first, together: the first four slices' list lengths and first entries, this thread's first four
-    // specials at or above the gate (segment s of the list is slice s's); all addresses in bounds
-    auto spec_slice = [&](int i) {
-        int lo = 0, hi = S;  // segoff[lo] <= i < segoff[lo + 1]
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (L.segoff[mid] <= i)
-                lo = mid;
-            else
-                hi = mid;
-        }
-        return lo;
-    };
-    auto spec_mass = [&](unsigned long long e) -> unsigned long long {
-        const float q = __uint_as_float((uint32_t)e);
-        return (!((uint32_t)(e >> 32) & kSelOnlyBit) && q >= thr) ? efx(q, md) : 0ull;
-    };
-    const char* rb0 = rec_base(G, R.row, 0);
-    int nl[4];
-    uint32_t lv[4];
-#pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        const char* rb = rb0 + (int64_t)min(u4, S - 1) * kRecBytes;
-        nl[u4] = pub_ld(&((const SliceRec*)rb)->nlump);
-        lv[u4] = pub_ld((const uint32_t*)(rb + kRecLumpOff) + tid);
-    }
-    int ssl[4];
-    unsigned long long se[4];
-#pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        const int i = u4 * kThreads + tid;
-        const int ic = i < ntot ? i : 0;
-        const int sl = spec_slice(ic);
-        se[u4] = pub_ld((const unsigned long long*)(rb0 + (int64_t)sl * kRecBytes + kRecSpecOff) + (ic - L.segoff[sl]));
-        ssl[u4] = i < ntot ? sl : -1;
-    }
-    // the masses of this thread's keys 2 i and 2 i + 1 (the loads land meanwhile)
-    unsigned long long mk[kMI][2];
-#pragma unroll
-    for (int mi = 0; mi < kMI; ++mi)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int k = 2 * (mi * kThreads + tid) + h;
-            mk[mi][h] = 0ull;
-            if (k >= k0 && k < kKeys && key_exact(k)) mk[mi][h] = efx(to_q<2>(R, key_bf(k)), md);
-        }
-    __syncthreads();  // L.slice_u cleared
-    MIS_STAMP(16);
-    // the first four slices in registers: counts by key, listed tiny values, specials
-    unsigned long long z4[4];
-#pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        z4[u4] = 0ull;
-        if (u4 >= S) continue;
-#pragma unroll
-        for (int mi = 0; mi < kMI; ++mi) {
-            const int i = mi * kThreads + tid;
-            const uint32_t c = i < kHistWords ? stc[u4 * kHistWords + i] : 0u;
-            z4[u4] += (unsigned long long)(c & 0xffffu) * mk[mi][0] + (unsigned long long)(c >> 16) * mk[mi][1];
-        }
-        const uint32_t* lst = (const uint32_t*)(rb0 + (int64_t)u4 * kRecBytes + kRecLumpOff);
-        for (int i = tid; i < nl[u4]; i += kThreads) {
-            const float x = __uint_as_float((i == tid ? lv[u4] : pub_ld(lst + i)) << 16);
-            if (x >= x0) z4[u4] += efx(to_q<2>(R, x), md);
-        }
-    }
-#pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        if (ssl[u4] < 0) continue;
-        const unsigned long long f = spec_mass(se[u4]);
-        if (ssl[u4] >= 4) {
-            if (f) atomicAdd(&L.slice_u[ssl[u4]], f);
-        } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                if (ssl[u4] == q) z4[q] += f;
-        }
-    }
-    for (int i = 4 * kThreads + tid; i < ntot; i += kThreads) {  // more than 4,096 specials at or above the gate
-        const int sl = spec_slice(i);
-        const unsigned long long f =
-            spec_mass(pub_ld((const unsigned long long*)(rb0 + (int64_t)sl * kRecBytes + kRecSpecOff) + (i - L.segoff[sl])));
-        if (f) atomicAdd(&L.slice_u[sl], f);
-    }
-    MIS_STAMP(21);
-#pragma unroll
-    for (int u4 = 0; u4 < 4; ++u4) {
-        if (u4 >= S) break;
-        const unsigned long long z = wave_reduce(z4[u4], [](unsigned long long a, unsigned long long b) { return a + b; });
-        if (l == 0 && z) atomicAdd(&L.slice_u[u4], z);
-    }
-    // slices 4 and on (vocabularies above four slices): counts and lists from their records
-    for (int s4 = 4; s4 < S; ++s4) {
-        const char* rb = rb0 + (int64_t)s4 * kRecBytes;
-        unsigned long long z = 0ull;
-#pragma unroll
-        for (int mi = 0; mi < kMI; ++mi) {
-            const int i = mi * kThreads + tid;
-            const uint32_t c = i < kHistWords ? pub_ld((const uint32_t*)(rb + kRecHistOff) + i) : 0u;
-            z += (unsigned long long)(c & 0xffffu) * mk[mi][0] + (unsigned long long)(c >> 16) * mk[mi][1];
-        }
-        const int n = pub_ld(&((const SliceRec*)rb)->nlump);
-        for (int i = tid; i < n; i += kThreads) {
-            const float x = __uint_as_float(pub_ld((const uint32_t*)(rb + kRecLumpOff) + i) << 16);
-            if (x >= x0) z += efx(to_q<2>(R, x), md);
-        }
-        z = wave_reduce(z, [](unsigned long long a, unsigned long long b) { return a + b; });
-        if (l == 0 && z) atomicAdd(&L.slice_u[s4], z);
-    }
-    MIS_STAMP(24);
-    __syncthreads();
-    if (w == 0) {
-        const unsigned long long zs = l < S ? L.slice_u[l] : 0ull;
-        const unsigned long long incl = wave_incl_scan(zs);
-        const unsigned long long Z = readlane_u64(incl, 63);
-        int hs = -1;
-        unsigned long long T2 = 0ull;
-        if (Z) {
-            const double pt = floor((double)u * (double)Z) + 1.0;
-            T2 = pt >= (double)Z ? Z : (unsigned long long)pt;
-            const uint64_t h = ballot(incl >= T2);
-            hs = __ffsll((long long)h) - 1;
-            if (l == hs) L.uscratch[1] = T2 - (incl - zs);
-        }
-        if (l == 0) L.token = hs;
-    }
-    __syncthreads();
-    holder = L.token;  // every later write of these words follows a barrier
-    rem = L.uscratch[1];
-    MIS_STAMP(14);
-    return holder >= 0 ? 2 : 1;
+    return md > -INFINITY ? 2 : 1;
 }
 
 __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
