@@ -253,6 +253,8 @@ struct Lds {
     unsigned long long tinyfx;               // slice phase: the histogram's tiny lumps
     unsigned long long uscratch[2];
     unsigned long long slice_u[kMaxSlices];  // finaliser: per-slice sums
+    int32_t qbin[4];                         // candidate finaliser: the bin of each question (-1: none)
+    unsigned long long qbefore[4];           // ... and the weight of the bins above it
     int32_t slice_n[kMaxSlices];             // finaliser (histogram path): specials each slice published
 };
 static_assert(sizeof(Lds) <= 160 * 1024, "LDS budget");
@@ -3111,30 +3113,6 @@ __device__ __forceinline__ int sel_bin(float q, const SelBins& B) {
     return max((int)f, 0);
 }
 
-// The bin at which the cumulative weight wt(b), taken from the highest bin down, first reaches T >= 1; `before` = the
-// weight of the bins above it, `total` = all of it.  -1 when the total is below T.  Every thread gets the result.
-template <class WT>
-__device__ __forceinline__ int sel_find_bin(WT&& wt, unsigned long long T, unsigned long long& before,
-                                            unsigned long long& total, Lds& L) {
-    const int tid = threadIdx.x;
-    const int b0 = kSelBins - 1 - 2 * tid, b1 = b0 - 1;
-    const unsigned long long w0 = wt(b0), w1 = wt(b1);
-    const unsigned long long mine = w0 + w1;
-    const unsigned long long ex = block_excl_scan(mine, total, L.red.u);
-    if (tid == 0) L.token = -1;
-    __syncthreads();
-    if (ex < T && T <= ex + mine) {
-        const bool first = ex + w0 >= T;
-        L.token = first ? b0 : b1;
-        L.uscratch[1] = first ? ex : ex + w0;
-    }
-    __syncthreads();
-    const int b = L.token;
-    before = L.uscratch[1];
-    __syncthreads();
-    return b;
-}
-
 // The elements of bin b sorted by value, descending (equal values in any order: they weigh alike): values in
 // L.ss.sq, set indices in L.ss.sw; returns their count, or -1 when more than kSelCap.
 __device__ __forceinline__ int sel_sort_bin(int b, int n, const SelBins& B, Lds& L) {
@@ -3206,15 +3184,65 @@ __device__ __forceinline__ int sel_cross(int m, unsigned long long before, unsig
     return r;
 }
 
+// The bins' counts and masses replaced by their sums over the bin and every bin above it (the highest bin first),
+// in one pass: each question below then finds its bin with one check per thread and no further scan.
+__device__ __forceinline__ void sel_prefix(Lds& L) {
+    const int tid = threadIdx.x, w = wave_id();
+    uint32_t* bc = L.ss.bcnt;
+    unsigned long long* bm = L.h.w;
+    const int b0 = kSelBins - 1 - 2 * tid, b1 = b0 - 1;
+    const unsigned long long c0 = bc[b0], c1 = bc[b1], m0 = bm[b0], m1 = bm[b1];
+    const unsigned long long ci = wave_incl_scan(c0 + c1), mi = wave_incl_scan(m0 + m1);
+    __syncthreads();
+    if (lane_id() == 63) {
+        L.h.scan[w] = ci;
+        L.red.u[w] = mi;
+    }
+    __syncthreads();
+    unsigned long long co = 0ull, mo = 0ull;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        co += i < w ? L.h.scan[i] : 0ull;
+        mo += i < w ? L.red.u[i] : 0ull;
+    }
+    const unsigned long long ce = co + ci - (c0 + c1), me = mo + mi - (m0 + m1);  // the bins above b0
+    bc[b0] = (uint32_t)(ce + c0);
+    bc[b1] = (uint32_t)(ce + c0 + c1);
+    bm[b0] = me + m0;
+    bm[b1] = me + m0 + m1;
+    __syncthreads();
+}
+
+// The bin at which the weight from the highest bin down first reaches T >= 1, from the inclusive sums incl(b): each
+// thread checks its two bins; the answer (-1 if the total is below T) and the weight above it go to slot q of
+// L.qbin / L.qbefore, which start at -1.  Every thread gets the result.
+template <class INCL>
+__device__ __forceinline__ int sel_find_prefix(INCL&& incl, unsigned long long T, unsigned long long& before, int q,
+                                               Lds& L) {
+    const int b0 = kSelBins - 1 - 2 * (int)threadIdx.x;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const int b = b0 - d;
+        const unsigned long long hi = incl(b), lo = b + 1 < kSelBins ? incl(b + 1) : 0ull;
+        if (lo < T && T <= hi) {
+            L.qbin[q] = b;
+            L.qbefore[q] = lo;
+        }
+    }
+    __syncthreads();
+    before = L.qbefore[q];
+    return L.qbin[q];
+}
+
 // The value at descending rank r (0-based) of the set (the k-th value, the min_keep floor), NaN if unresolved; its
 // bin stays sorted in L.ss (m elements), `above` = how many elements of the set exceed the value, f = the first
 // position of the value in the sorted bin.
-__device__ __forceinline__ float sel_rank_value(int r, int n, const SelBins& B, Lds& L, int& m, int& f,
+__device__ __forceinline__ float sel_rank_value(int r, int n, const SelBins& B, Lds& L, int q, int& m, int& f,
                                                 unsigned long long& above) {
-    unsigned long long before, tot;
-    const uint32_t* bc = L.ss.bcnt;
-    const int b = sel_find_bin([&](int x) { return (unsigned long long)bc[x]; }, (unsigned long long)r + 1ull,
-                               before, tot, L);
+    unsigned long long before;
+    const uint32_t* bc = L.ss.bcnt;  // counts summed from the highest bin down (sel_prefix)
+    const int b = sel_find_prefix([&](int x) { return (unsigned long long)bc[x]; }, (unsigned long long)r + 1ull,
+                                  before, q, L);
     m = -1;
     MIS_STAMP(22);
     if (b < 0) return __uint_as_float(0x7fc00000u);
@@ -3243,12 +3271,13 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
     if (w == 0) {
         // records (lane s: slice s) and segment counts (lane l: segments [l * per, (l + 1) * per)); the draw's
         // uniform after their loads are issued
-        float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
+        float mq = -INFINITY, mqd = -INFINITY, gt = -INFINITY, mr = -INFINITY;
         double zz = 0.0, zcc = 0.0;
         int over = 0, notinf = 0;
         if (l < S) {
             const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
             mq = pub_ld(&rec->mq);
+            mqd = pub_ld(&rec->mqd);
             gt = pub_ld(&rec->gate);
             mr = pub_ld(&rec->mref);
             zz = pub_ld(&rec->z);
@@ -3274,6 +3303,7 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
         }
         const float u = row_uniform(G, R);
         const float m_sel = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
+        const float m_draw = wave_reduce(mqd, [](float a, float b) { return fmaxf(a, b); });
         const float gate = wave_reduce(gt, [](float a, float b) { return fmaxf(a, b); });
         const float gmin = wave_reduce(l < S ? gt : INFINITY, [](float a, float b) { return fminf(a, b); });
         const int anyover = wave_reduce(over, [](int a, int b) { return max(a, b); });
@@ -3302,7 +3332,10 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
             L.fscratch[2] = u;
             L.fscratch[3] = gmin;
             L.dscratch[0] = zs;
+            L.dscratch[2] = (double)m_draw;
             L.token = anyover | short_mass;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) L.qbin[q] = -1;
             L.is_last = anyfin;
         }
     }
@@ -3407,6 +3440,7 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
         if (ms) atomicAdd(&bm[b], ms);
     }
     __syncthreads();
+    sel_prefix(L);
     MIS_STAMP(16);
     const bool topk = R.kk < R.V;
     // the k-th value (engine/talker_sampler.py:95-98, :119-133): ties at it count once per rank
@@ -3415,7 +3449,7 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
     int bk = -1, mk = 0, fk = 0;
     if (topk) {
         if (R.kk <= n) {
-            kth = sel_rank_value(R.kk - 1, n, B, L, mk, fk, cnt_gt);
+            kth = sel_rank_value(R.kk - 1, n, B, L, 0, mk, fk, cnt_gt);
             if (!(kth >= gate)) return false;  // NaN (unresolved) included
             bk = sel_bin(kth, B);              // its sorted elements stay in L.ss
         } else if (!ginf) {
@@ -3435,23 +3469,22 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
             if (tid < fk) mine = L.a.w.mass[(int)L.ss.sw[tid]];
             gtk = block_sum_u(mine, L.red);
         }
-        auto wt = [&](int b) -> unsigned long long {
+        // the weight from the highest bin down: the masses above bin bk, then bk's weight, then nothing
+        const unsigned long long above_k = bk >= 0 ? (bk + 1 < kSelBins ? bm[bk + 1] : 0ull) : 0ull;
+        auto wincl = [&](int b) -> unsigned long long {
             if (bk < 0 || b > bk) return bm[b];
-            return b == bk ? gtk + vw : 0ull;
+            return above_k + gtk + vw;
         };
         // the normaliser: the top-k mass (omni order with top-k), else the whole row's
         double zn;
-        if (topk && !R.hf) {
-            unsigned long long t2 = 0ull;
-            for (int b = tid; b < kSelBins; b += kThreads) t2 += wt(b);
-            zn = (double)block_sum_u(t2, L.red);
-        } else {
+        if (topk && !R.hf)
+            zn = (double)(bk >= 0 ? above_k + gtk + vw : bm[0]);
+        else
             zn = zfull_fx;
-        }
         const double pt = ceil((double)R.top_p * zn);
         const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
-        unsigned long long before, tot;
-        const int bp = sel_find_bin(wt, T, before, tot, L);
+        unsigned long long before;
+        const int bp = sel_find_prefix(wincl, T, before, 1, L);
         float thr_p;
         if (bp >= 0) {
             // the bin's elements by value with their weights (bin bk is sorted already)
@@ -3479,7 +3512,7 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
             } else {
                 int m2, f2;
                 unsigned long long a2;
-                vmk = sel_rank_value(R.min_keep_eff - 1, n, B, L, m2, f2, a2);
+                vmk = sel_rank_value(R.min_keep_eff - 1, n, B, L, 2, m2, f2, a2);
                 if (!(vmk >= gate)) return false;
             }
         }
@@ -3487,14 +3520,12 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
         if (topk) thr = fmaxf(thr, kth);
     }
     MIS_STAMP(19);
-    // survivors: drawable, q >= thr; masses relative to the largest of them
+    // survivors: drawable, q >= thr; masses relative to the largest of them, the row's largest drawable value (a
+    // slice's largest drawable value is at or above its gate, so it is among the candidates, and thr is at or above
+    // every gate)
     const uint32_t thrkey = ord_key(thr);
-    float md = -INFINITY;
-    for (int i = tid; i < n; i += kThreads) {
-        const float q = L.a.w.q[i];
-        if (ord_key(q) >= thrkey && !(L.a.w.id[i] & kSelOnlyBit)) md = fmaxf(md, q);
-    }
-    md = block_max4(make_float4(md, -INFINITY, -INFINITY, -INFINITY), L.red).x;
+    const float m_draw = (float)L.dscratch[2];
+    const float md = m_draw >= thr ? m_draw : -INFINITY;
     out.thr = thr;
     out.mdraw = md;
     if (!(md > -INFINITY)) return true;
