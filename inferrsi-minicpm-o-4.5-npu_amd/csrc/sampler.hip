@@ -3535,18 +3535,20 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
         if (!(ord_key(q) >= thrkey) || (L.a.w.id[i] & kSelOnlyBit)) return 0ull;
         return md_is_m ? L.a.w.mass[i] : efx(q, md);
     };
-    // the draw (engine/talker_sampler.py:161-172) in token order: the specials (ids in their slices' ranges, in any
-    // order) are ranked by id and summed in that order; thread t then walks tile candidates [t c, (t + 1) c) with
-    // the specials below each id found by binary search, and leaves the tile's running sum in place of the masses
-    // for the specials' own search
+    // the draw (engine/talker_sampler.py:161-172) in token order: the surviving specials (ids in their slices'
+    // ranges, in any order) are ranked by id; thread t then walks tile candidates [t c, (t + 1) c) merged with the
+    // specials whose ids fall between its first candidate and the next thread's (thread 0 from the lowest id, the
+    // last thread with candidates to the highest), from the mass of everything before them
     MIS_STAMP(20);
     const int nb = n - na;
     uint32_t* bids = (uint32_t*)L.ss.cq;  // the surviving specials' ids, ascending
-    unsigned long long* bpre = L.ss.cw;  // inclusive sums of their masses in that order
-    // the specials that survive (few), ranked by id
+    unsigned long long* bw = L.ss.cw;     // their masses in that order
     const unsigned long long wsp = tid < nb ? wsurv(na + tid) : 0ull;
     const uint32_t sid = tid < nb ? (L.a.w.id[na + tid] & ~kSelOnlyBit) : 0u;
-    if (tid == 0) L.scnt = 0;
+    if (tid == 0) {
+        L.scnt = 0;
+        L.uscratch[0] = ~0ull;
+    }
     __syncthreads();
     const int slot = lds_reserve(wsp != 0ull, &L.scnt);
     if (wsp) {
@@ -3555,87 +3557,80 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
     }
     __syncthreads();
     const int nbs = L.scnt;
-    uint32_t myid = 0u;
-    unsigned long long myw = 0ull;
+    unsigned long long* bpe = L.ss.sw;  // (after the ranking) the mass of the surviving specials of lower id
     int myr = -1;
+    unsigned long long below = 0ull;
     if (tid < nbs) {
-        myid = L.ss.bcnt[tid];
-        myw = L.ss.sw[tid];
+        const uint32_t myid = L.ss.bcnt[tid];
+        const unsigned long long myw = L.ss.sw[tid];
         int r = 0;
         for (int j0 = 0; j0 < nbs; j0 += 8) {  // ids are distinct; eight read together
             uint32_t c[8];
+            unsigned long long cw8[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) c[e] = L.ss.bcnt[min(j0 + e, nbs - 1)];
+            for (int e = 0; e < 8; ++e) {
+                c[e] = L.ss.bcnt[min(j0 + e, nbs - 1)];
+                cw8[e] = L.ss.sw[min(j0 + e, nbs - 1)];
+            }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) r += (j0 + e < nbs && c[e] < myid) ? 1 : 0;
+            for (int e = 0; e < 8; ++e) {
+                const bool lt = j0 + e < nbs && c[e] < myid;
+                r += lt ? 1 : 0;
+                below += lt ? cw8[e] : 0ull;
+            }
         }
-        myr = r;
         bids[r] = myid;
+        bw[r] = myw;
+        myr = r;
     }
     __syncthreads();
-    if (myr >= 0) L.ss.sw[myr] = myw;
-    __syncthreads();
-    const unsigned long long wsorted = tid < nbs ? L.ss.sw[tid] : 0ull;
-    unsigned long long zsb, zsa;
-    const unsigned long long exb = block_excl_scan(wsorted, zsb, L.red.u);
-    if (tid < nbs) bpre[tid] = exb + wsorted;
+    if (myr >= 0) bpe[myr] = below;
     const int cpt = (na + kThreads - 1) / kThreads;
+    const int i0 = tid * cpt, i1 = min(na, i0 + cpt);
     unsigned long long own = 0ull;
-    for (int j = 0; j < cpt; ++j) {
-        const int i = tid * cpt + j;
-        if (i < na) own += wsurv(i);
-    }
-    const unsigned long long exa = block_excl_scan(own, zsa, L.red.u);  // its barriers also publish bpre
+    for (int i = i0; i < i1; ++i) own += wsurv(i);
+    unsigned long long zsa;
+    const unsigned long long exa = block_excl_scan(own, zsa, L.red.u);  // its barriers also publish bids, bw, bpe
+    const unsigned long long zsb = nbs ? bpe[nbs - 1] + bw[nbs - 1] : 0ull;
     const unsigned long long zs = zsa + zsb;
     if (zs == 0ull) return true;
     const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
     MIS_STAMP(21);
-    if (tid == 0) L.uscratch[0] = ~0ull;
-    auto spec_below = [&](uint32_t x) -> unsigned long long {  // mass of the surviving specials with id < x
-        int lo = 0, hi = nbs;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (bids[mid] < x)
-                lo = mid + 1;
-            else
-                hi = mid;
-        }
-        return lo > 0 ? bpre[lo - 1] : 0ull;
-    };
-    __syncthreads();
-    // the tile candidates in token order, thread t walking [t c, (t + 1) c); its running sum left in place of the
-    // masses for the specials' search
-    if (own || nbs) {
-        unsigned long long c = exa;
-        for (int j = 0; j < cpt; ++j) {
-            const int i = tid * cpt + j;
-            if (i >= na) break;
-            const unsigned long long wi = wsurv(i);
-            c += wi;
-            if (wi) {
-                const uint32_t id = L.a.w.id[i] & ~kSelOnlyBit;
-                const unsigned long long cum = c + (nbs ? spec_below(id) : 0ull);
-                if (cum >= T2 && cum - wi < T2) L.uscratch[0] = id;
+    // this thread's stretch of token order: its candidates and the specials with ids in [lo_id, hi_id)
+    const bool first_t = tid == 0, last_t = i1 >= na;
+    if (i0 < i1 || (first_t && na == 0)) {
+        const uint32_t lo_id = first_t ? 0u : (L.a.w.id[i0] & ~kSelOnlyBit);
+        const uint32_t hi_id = last_t ? 0xffffffffu : (L.a.w.id[i1] & ~kSelOnlyBit);
+        int p = 0;  // the first special with id >= lo_id
+        {
+            int hi = nbs;
+            while (p < hi) {
+                const int mid = (p + hi) >> 1;
+                if (bids[mid] < lo_id)
+                    p = mid + 1;
+                else
+                    hi = mid;
             }
-            L.a.w.mass[i] = c;
         }
+        unsigned long long c = exa + (p < nbs ? bpe[p] : zsb);  // and the specials before the stretch
+        bool hit = false;
+        uint32_t tok = 0u;
+        auto step = [&](unsigned long long wgt, uint32_t id) {
+            if (!hit && wgt && c < T2 && T2 <= c + wgt) {
+                hit = true;
+                tok = id;
+            }
+            c += wgt;
+        };
+        for (int i = i0; i < i1; ++i) {
+            const uint32_t id = L.a.w.id[i] & ~kSelOnlyBit;
+            for (; p < nbs && bids[p] < id; ++p) step(bw[p], bids[p]);
+            step(wsurv(i), id);
+        }
+        for (; p < nbs && bids[p] < hi_id; ++p) step(bw[p], bids[p]);
+        if (hit) L.uscratch[0] = tok;
     }
     MIS_STAMP(25);
-    __syncthreads();
-    MIS_STAMP(12);
-    if (tid < nbs) {
-        const uint32_t id = bids[tid];
-        int lo = 0, hi = na;  // tile candidates with id < this one
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if ((L.a.w.id[mid] & ~kSelOnlyBit) < id)
-                lo = mid + 1;
-            else
-                hi = mid;
-        }
-        const unsigned long long cum = (lo > 0 ? L.a.w.mass[lo - 1] : 0ull) + exb + wsorted;
-        if (cum >= T2 && cum - wsorted < T2) L.uscratch[0] = id;
-    }
     __syncthreads();
     MIS_STAMP(13);
     if (L.uscratch[0] == ~0ull) return false;
