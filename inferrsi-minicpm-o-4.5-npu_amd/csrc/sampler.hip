@@ -3647,7 +3647,19 @@ __device__ __forceinline__ bool fin_sel(const DevGroup& G, const Row& R, Lds& L,
 __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, const Row& R, Lds& L,
                                         Outcome& out) {
     const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
-    if (tid == 0) L.fscratch[3] = row_uniform(G, R);  // the draw's
+    // the first four slices' counts, loaded ahead of the records (their addresses need nothing from them)
+    constexpr int kMI = (kHistWords + kThreads - 1) / kThreads;
+    uint32_t hv[kMI][4];
+#pragma unroll
+    for (int mi = 0; mi < kMI; ++mi) {
+        const int i = mi * kThreads + tid;
+#pragma unroll
+        for (int u4 = 0; u4 < 4; ++u4)
+            hv[mi][u4] = (i < kHistWords && u4 < S)
+                             ? pub_ld((const uint32_t*)(rec_base(G, R.row, u4) + kRecHistOff) + i)
+                             : 0u;
+    }
+    if (tid == kThreads - 64) L.fscratch[3] = row_uniform(G, R);  // the draw's, off wave 0's path
     if (w == 0) {  // lane s reads slice s's record
         float mq = -INFINITY, mqd = -INFINITY, mr = -INFINITY, hb = -INFINITY;
         double zz = 0.0;
@@ -3699,19 +3711,8 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
     if (!(m > -INFINITY)) return 1;
     // md to the waiting slices, which build their mass tables while the cut is settled here
     if (S > 1 && mdraw > -INFINITY) r2_decide(A, R, 3u, 0.f, mdraw, 0.f, 0.f);
-    // every slice's counts, merged: the first four slices' loads are in flight while the mass table is built
+    // every slice's counts, merged
     uint32_t* cnt = (uint32_t*)L.h.w;
-    constexpr int kMI = (kHistWords + kThreads - 1) / kThreads;
-    uint32_t hv[kMI][4];
-#pragma unroll
-    for (int mi = 0; mi < kMI; ++mi) {
-        const int i = mi * kThreads + tid;
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4)
-            hv[mi][u4] = (i < kHistWords && u4 < S)
-                             ? pub_ld((const uint32_t*)(rec_base(G, R.row, u4) + kRecHistOff) + i)
-                             : 0u;
-    }
 #pragma unroll
     for (int mi = 0; mi < kMI; ++mi) {
         const int i = mi * kThreads + tid;
