@@ -3958,49 +3958,76 @@ __device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds&
 
 // Unfiltered rows: walk the slices' totals, then the chosen slice's sub-block sums, to the sub-block holding
 // u * Z, and rescan it element by element.
+__device__ __forceinline__ double readlane_d(double x, int lane) {
+    return __longlong_as_double((long long)readlane_u64((unsigned long long)__double_as_longlong(x), lane));
+}
+
+// Unfiltered rows: the slice that holds the target (from the slices' sums of exp), its sub-block (from the slice's
+// sub-block sums), both on wave 0 without a workgroup barrier; then the sub-block's elements, one per thread, and the
+// token from their masses on wave 0.
 __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
     const int E = 16 / G.es;
     const int nsb = kWaves * G.R;
-    const int tid = threadIdx.x;
-    float mr = -INFINITY;
-    double z = 0.0;
-    if (tid < R.S) {
-        const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, tid);
-        mr = pub_ld(&rec->mref);
-        z = pub_ld(&rec->z);
+    const int tid = threadIdx.x, l = lane_id();
+    if (wave_id() == 0) {
+        float mr = -INFINITY;
+        double z = 0.0;
+        if (l < R.S) {  // lane s: slice s
+            const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
+            mr = pub_ld(&rec->mref);
+            z = pub_ld(&rec->z);
+        }
+        const float u = row_uniform(G, R);
+        const float m = wave_reduce(mr, [](float a, float b) { return fmaxf(a, b); });
+        const double sc = (mr > -INFINITY && m > -INFINITY) ? exp((double)mr - (double)m) : 0.0;
+        const double zsl = z * sc;
+        const double incl = wave_incl_scan(zsl);
+        const double t = (double)u * readlane_d(incl, 63);
+        const uint64_t hs = ballot(l < R.S && incl > t), hm = ballot(l < R.S && zsl > 0.0);
+        // the first slice whose inclusive sum passes t, else (rounding) the last with mass
+        const int ss = hs ? __ffsll((long long)hs) - 1 : (hm ? 63 - __clzll((long long)hm) : -1);
+        int kb = -1;
+        double rem2 = 0.0;
+        float mref = -INFINITY;
+        if (ss >= 0 && m > -INFINITY) {
+            const double sc_s = readlane_d(sc, ss), zs = readlane_d(zsl, ss);
+            const double rem = fmin((t - (readlane_d(incl, ss) - zs)) / sc_s, zs / sc_s);  // in the slice's units
+            const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, ss);
+            mref = pub_ld(&rec->mref);
+            const double* sbg = (const double*)((const char*)rec + kRecSbOff);
+            const double v0 = l < nsb ? pub_ld(sbg + l) : 0.0;
+            const double v1 = 64 + l < nsb ? pub_ld(sbg + 64 + l) : 0.0;
+            const double i0 = wave_incl_scan(v0);
+            const double i1 = wave_incl_scan(v1) + readlane_d(i0, 63);
+            const uint64_t h0 = ballot(l < nsb && i0 > rem), h1 = ballot(64 + l < nsb && i1 > rem);
+            const uint64_t g0 = ballot(l < nsb && v0 > 0.0), g1 = ballot(64 + l < nsb && v1 > 0.0);
+            if (h0 || h1) {
+                kb = h0 ? __ffsll((long long)h0) - 1 : 64 + __ffsll((long long)h1) - 1;
+            } else if (g0 || g1) {  // rounding: the last sub-block with mass
+                kb = g1 ? 64 + 63 - __clzll((long long)g1) : 63 - __clzll((long long)g0);
+            }
+            if (kb >= 0) {
+                const double ik = kb < 64 ? readlane_d(i0, kb) : readlane_d(i1, kb - 64);
+                const double vk = kb < 64 ? readlane_d(v0, kb) : readlane_d(v1, kb - 64);
+                rem2 = rem - (ik - vk);
+            }
+        }
+        if (l == 0) {
+            L.token = kb >= 0 ? ss : -1;
+            L.scnt = kb;
+            L.dscratch[2] = rem2;
+            L.fscratch[0] = m;
+            L.fscratch[1] = mref;
+        }
     }
-    const float m = block_max_f(mr, L.red);
+    __syncthreads();
+    const int ss = L.token, kb = L.scnt;
+    const double rem = L.dscratch[2];
+    const float m = L.fscratch[0], mref = L.fscratch[1];
     out.thr = -INFINITY;
     out.mdraw = m;
     out.token = R.V - 1;
-    if (!(m > -INFINITY)) return;
-    const double sc = (mr > -INFINITY) ? exp((double)mr - (double)m) : 0.0;
-    const double zsl = z * sc;
-    const double Z = block_sum_d(zsl, L.red);
-    const double t = (double)row_uniform(G, R) * Z;
-    // the slice: first s with inclusive prefix > t (else the last slice with mass)
-    double incl = block_incl_scan_d(tid < R.S ? zsl : 0.0, L.red);
-    int ss = block_min_i((tid < R.S && incl > t) ? tid : INT_MAX, L.red);
-    if (ss == INT_MAX) ss = block_max_i((tid < R.S && zsl > 0.0) ? tid : -1, L.red);
-    if (ss < 0) return;
-    if (tid == ss) {
-        L.dscratch[0] = (t - (incl - zsl)) / sc;  // the target inside slice ss, in its own units
-        L.dscratch[1] = zsl / sc;
-    }
-    __syncthreads();
-    double rem = fmin(L.dscratch[0], L.dscratch[1]);
-    const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, ss);
-    const float mref = pub_ld(&rec->mref);
-    const double* sbg = (const double*)((const char*)rec + kRecSbOff);
-    const double v = tid < nsb ? pub_ld(sbg + tid) : 0.0;
-    incl = block_incl_scan_d(v, L.red);
-    int kb = block_min_i((tid < nsb && incl > rem) ? tid : INT_MAX, L.red);
-    if (kb == INT_MAX) kb = block_max_i((tid < nsb && v > 0.0) ? tid : -1, L.red);
-    if (kb < 0) return;
-    __syncthreads();
-    if (tid == kb) L.dscratch[2] = rem - (incl - v);
-    __syncthreads();
-    rem = L.dscratch[2];
+    if (!(m > -INFINITY) || ss < 0) return;
     const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
     const int first = slice_first(G, R.row, slo);
     Visit V;
@@ -4013,13 +4040,39 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
     V.m = mref;
     V.d0 = 0.0;
     V.i0 = -1;
-    visit(V, G, R, L);
-    const double e = V.d0;
-    const int myj = V.i0;
-    incl = block_incl_scan_d(e, L.red);
-    int tok = block_min_i((myj >= 0 && e > 0.0 && incl > rem) ? myj : INT_MAX, L.red);
-    if (tok == INT_MAX) tok = block_max_i((myj >= 0 && e > 0.0) ? myj : -1, L.red);  // rounding: the last with mass
-    if (tok >= 0) out.token = tok;
+    visit(V, G, R, L);  // ends with a barrier
+    // the sub-block's masses in element order (at most 512), then the token on wave 0: lane l sums elements
+    // [8 l, 8 l + 8)
+    double* pe = (double*)L.h.w;
+    if (tid < 512) pe[tid] = (V.i0 >= 0) ? V.d0 : 0.0;
+    if (tid == 0) L.uscratch[0] = ~0ull;
+    __syncthreads();
+    if (wave_id() == 0) {
+        const int nel = V.hi - V.lo;
+        double e8[8], own = 0.0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            e8[e] = 8 * l + e < nel ? pe[8 * l + e] : 0.0;
+            own += e8[e];
+        }
+        const double incl = wave_incl_scan(own);
+        const uint64_t hit = ballot(own > 0.0 && incl > rem);
+        const uint64_t any = ballot(own > 0.0);
+        const int hl = hit ? __ffsll((long long)hit) - 1 : (any ? 63 - __clzll((long long)any) : -1);
+        if (l == hl) {
+            double c = incl - own;
+            int pick = -1;
+            for (int e = 0; e < 8; ++e) {
+                if (!(e8[e] > 0.0)) continue;
+                pick = e;
+                c += e8[e];
+                if (hit && c > rem) break;  // else (rounding) the last with mass
+            }
+            if (pick >= 0) L.uscratch[0] = (unsigned long long)(V.lo + 8 * l + pick);
+        }
+    }
+    __syncthreads();
+    if (L.uscratch[0] != ~0ull) out.token = (int64_t)L.uscratch[0];
 }
 
 // Processed logits and probabilities of the whole row (parity outputs), streamed.
