@@ -1313,8 +1313,10 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
         clear_keep_bit(L, geo.first, eos);
         if (R.eos_rule == kEosSelOnly) {
             const int slot = atomicAdd(&L.nspec, 1);
-            L.spec[slot].j = eos;
-            L.spec[slot].sel = 1;
+            if (slot < kSpecCap) {  // beyond the list the row is flagged and finalised from its logits
+                L.spec[slot].j = eos;
+                L.spec[slot].sel = 1;
+            }
         }
     }
     if (R.pen) {
@@ -3942,18 +3944,28 @@ __device__ __forceinline__ int fin_hist(const KernelArgs& A, const DevGroup& G, 
     return md > -INFINITY ? 2 : 1;
 }
 
-__device__ __forceinline__ void fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
+// Greedy rows: the first argmax over the slices' maxima.  False when a slice's history ids overflowed its list of
+// specials (some of its values went unpenalised): the row is then streamed.
+__device__ __forceinline__ bool fin_greedy(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
     float v = -INFINITY;
     int idx = INT_MAX;
+    bool over = false;
     if ((int)threadIdx.x < R.S) {
         const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, threadIdx.x);
         v = pub_ld(&rec->mqd);
         idx = pub_ld(&rec->argmax);
+        over = (pub_ld(&rec->flags) & kRecOverflow) != 0;
     }
-    block_argmax(v, idx, L.red);
+    if (wave_id() == 0) {  // R.S <= 64: every slice on wave 0
+        const uint64_t b = ballot(over);
+        if (lane_id() == 0) L.token = b != 0;
+    }
+    block_argmax(v, idx, L.red);  // its barriers publish L.token
+    if (L.token) return false;
     out.token = v > -INFINITY ? idx : 0;
     out.thr = -INFINITY;
     out.mdraw = v;
+    return true;
 }
 
 // Unfiltered rows: walk the slices' totals, then the chosen slice's sub-block sums, to the sub-block holding
@@ -3964,19 +3976,23 @@ __device__ __forceinline__ double readlane_d(double x, int lane) {
 
 // Unfiltered rows: the slice that holds the target (from the slices' sums of exp), its sub-block (from the slice's
 // sub-block sums), both on wave 0 without a workgroup barrier; then the sub-block's elements, one per thread, and the
-// token from their masses on wave 0.
-__device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
+// token from their masses on wave 0.  False (the row is streamed) when a slice's history ids overflowed its list of
+// specials.
+__device__ __forceinline__ bool fin_full(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
     const int E = 16 / G.es;
     const int nsb = kWaves * G.R;
     const int tid = threadIdx.x, l = lane_id();
     if (wave_id() == 0) {
         float mr = -INFINITY;
         double z = 0.0;
+        bool over = false;
         if (l < R.S) {  // lane s: slice s
             const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
             mr = pub_ld(&rec->mref);
             z = pub_ld(&rec->z);
+            over = (pub_ld(&rec->flags) & kRecOverflow) != 0;
         }
+        const bool anyover = ballot(over) != 0;
         const float u = row_uniform(G, R);
         const float m = wave_reduce(mr, [](float a, float b) { return fmaxf(a, b); });
         const double sc = (mr > -INFINITY && m > -INFINITY) ? exp((double)mr - (double)m) : 0.0;
@@ -4013,7 +4029,7 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
             }
         }
         if (l == 0) {
-            L.token = kb >= 0 ? ss : -1;
+            L.token = anyover ? -2 : (kb >= 0 ? ss : -1);
             L.scnt = kb;
             L.dscratch[2] = rem2;
             L.fscratch[0] = m;
@@ -4024,10 +4040,11 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
     const int ss = L.token, kb = L.scnt;
     const double rem = L.dscratch[2];
     const float m = L.fscratch[0], mref = L.fscratch[1];
+    if (ss == -2) return false;
     out.thr = -INFINITY;
     out.mdraw = m;
     out.token = R.V - 1;
-    if (!(m > -INFINITY) || ss < 0) return;
+    if (!(m > -INFINITY) || ss < 0) return true;
     const int slo = ss * G.slice_len, shi = min(R.V, slo + G.slice_len);
     const int first = slice_first(G, R.row, slo);
     Visit V;
@@ -4073,6 +4090,7 @@ __device__ __forceinline__ void fin_full(const DevGroup& G, const Row& R, Lds& L
     }
     __syncthreads();
     if (L.uscratch[0] != ~0ull) out.token = (int64_t)L.uscratch[0];
+    return true;
 }
 
 // Processed logits and probabilities of the whole row (parity outputs), streamed.
@@ -4168,11 +4186,11 @@ __device__ __forceinline__ void finalize(const DevGroup& G, const Row& R, Lds& L
     if (!forced) {
         int mode = L.foreign ? kStream : R.mode;
         if (mode == kGreedy) {
-            fin_greedy(G, R, L, o);
             path = MIS_PATH_GREEDY;
+            if (!fin_greedy(G, R, L, o)) mode = kStream;
         } else if (mode == kFull) {
-            fin_full(G, R, L, o);
             path = MIS_PATH_FULL;
+            if (!fin_full(G, R, L, o)) mode = kStream;
         } else if (mode == kTopK || mode == kNucleus) {
             path = MIS_PATH_CANDIDATES;
             if (!fin_sel(G, R, L, o)) mode = kStream;

@@ -211,6 +211,37 @@ def test_histogram_rows_with_values_at_zero(case):
         assert paths["histogram"] == rows and paths["stream"] == 0
 
 
+def test_histories_with_more_distinct_ids_than_a_slice_lists():
+    """A 60,000-id history holding 40% of the vocabulary: every slice meets more distinct history ids than its list
+    of penalised values holds (2,048), for a greedy row, an unfiltered row, a top-k row and a top-p row.  The history
+    ids carry the largest logits, so a value left unpenalised would win; every such row is streamed instead."""
+    print("[gpu] overflowing specials", flush=True)
+    gen = torch.Generator().manual_seed(61)
+    rows, v = 4, W.THINKER_V
+    hist = torch.randperm(v, generator=gen)[:60000].to(torch.int32).repeat(rows, 1)
+    x = torch.randn(rows, v, generator=gen) * 2.0
+    x[:, hist[0].long()] += 6.0
+    x = x.to(torch.bfloat16)
+    temps = torch.tensor([0.0, 1.0, 1.0, 1.0])
+    top_k = torch.tensor([0, 0, 50, 0], dtype=torch.int32)
+    top_p = torch.tensor([1.0, 1.0, 1.0, 0.9])
+    one = lambda val, dt=torch.float32: torch.full((rows,), val, dtype=dt)  # noqa: E731
+    ref_rows = ext.Rows(logits=x, temperature=temps, top_k=top_k, top_p=top_p, repetition=one(1.5),
+                        presence=one(1.0), frequency=one(0.25), history=hist, seeds=one(11, torch.int64),
+                        steps=one(3, torch.int64))
+    g = G.RowGroup(x.to(DEV), temperature=temps.to(DEV), top_k=top_k.to(DEV), top_p=top_p.to(DEV), repetition=1.5,
+                   presence=1.0, frequency=0.25, history=hist.to(DEV), seeds=one(11, torch.int64).to(DEV),
+                   steps=one(3, torch.int64).to(DEV), processed=True, probs=True)
+    _lib.reset_path_counters(DEV)
+    G.launch([g])
+    torch.cuda.synchronize()
+    paths = _lib.path_counters(DEV)
+    print(f"[gpu] overflowing specials paths {paths}", flush=True)
+    compare_group("overflowing_specials", g.tokens, g.processed, g.probs, ext.sample_rows(ref_rows), ref_rows,
+                  prob_rtol=2e-3)
+    assert paths["stream"] == rows
+
+
 def test_thinker_greedy_is_first_argmax_at_full_size():
     wl = W.thinker_b64().to(DEV)
     x = wl.logits.clone()
