@@ -1358,13 +1358,11 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     __syncthreads();
     MIS_STAMP(3);
 
-    // pass 1: keep bits applied; lane max (and first argmax for greedy rows) in the tile's domain
+    // pass 1: keep bits applied; lane max (and first argmax for greedy rows) in the tile's domain.  One loop per
+    // kind of row, each taking a chunk's maximum as a tree.
     float lmax = -INFINITY;
     int larg = INT_MAX;
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-        if (r >= RR) continue;
-        const int c = (w * RR + r) * 64 + l;
+    auto masked = [&](int r, int c) {
         const uint32_t kb = chunk_keep<ES>(L, geo.first, c);
         uint4 v = t[r];
         if (ES == 2) {
@@ -1379,17 +1377,39 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             v = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
         }
         t[r] = v;
+        return v;
+    };
+    auto chunk_max = [&](const uint4& v) {
+        float m[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const float x = tile_val<ES>(v, e);
-            if (R.mode == kGreedy) {
-                if (x > lmax) {
-                    lmax = x;
-                    larg = geo.first + c * E + e;
-                }
-            } else {
-                lmax = fmaxf(lmax, x);
+        for (int e = 0; e < E; ++e) m[e] = tile_val<ES>(v, e);
+#pragma unroll
+        for (int h = E / 2; h >= 1; h /= 2)
+#pragma unroll
+            for (int e = 0; e < h; ++e) m[e] = fmaxf(m[e], m[e + h]);
+        return m[0];
+    };
+    if (R.mode == kGreedy) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            if (r >= RR) continue;
+            const int c = (w * RR + r) * 64 + l;
+            const uint4 v = masked(r, c);
+            const float cm = chunk_max(v);
+            if (cm > lmax) {  // the chunk's first element at its maximum (NaN never wins)
+                int e0 = E - 1;
+#pragma unroll
+                for (int e = E - 1; e >= 0; --e) e0 = tile_val<ES>(v, e) == cm ? e : e0;
+                lmax = cm;
+                larg = geo.first + c * E + e0;
             }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            if (r >= RR) continue;
+            const int c = (w * RR + r) * 64 + l;
+            lmax = fmaxf(lmax, chunk_max(masked(r, c)));
         }
     }
     // the specials' processed values
