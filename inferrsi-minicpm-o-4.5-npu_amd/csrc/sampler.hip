@@ -423,11 +423,6 @@ __device__ __forceinline__ float load_elem(const DevGroup& G, int row, int j) {
     return *gp((const float*)p);
 }
 
-__device__ __forceinline__ bool allowed_bit(const DevGroup& G, int row, int j) {
-    if (!G.allowed) return true;
-    return (gp(G.allowed)[(int64_t)row * G.allowed_stride + (j >> 5)] >> (j & 31)) & 1u;
-}
-
 __device__ __forceinline__ const char* hist_row(const DevGroup& G, int row) {
     return G.history + (int64_t)row * G.hist_stride * (G.hist_i64 ? 8 : 4);
 }
@@ -1305,18 +1300,17 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     if (tid < kMaxSB) L.sbfx[tid] = 0ull;
     if (tid < 256) L.gh[tid] = 0u;
     __syncthreads();
-    // the history: counts and first occurrences (specials); a censored EOS is taken out of the tile (and listed as a
-    // special when it ranks but is not drawn)
+    // the history: counts and first occurrences (specials); a censored EOS is taken out of the tile (listed as a
+    // special when it ranks but is not drawn, which takes it out with the other specials)
     const int eos = G.eos;
     const bool eos_here = eos >= lo && eos < hi && R.eos_rule != kEosNormal;
     if (eos_here && tid == 0) {
-        clear_keep_bit(L, geo.first, eos);
-        if (R.eos_rule == kEosSelOnly) {
-            const int slot = atomicAdd(&L.nspec, 1);
-            if (slot < kSpecCap) {  // beyond the list the row is flagged and finalised from its logits
-                L.spec[slot].j = eos;
-                L.spec[slot].sel = 1;
-            }
+        const int slot = R.eos_rule == kEosSelOnly ? atomicAdd(&L.nspec, 1) : kSpecCap;
+        if (slot < kSpecCap) {
+            L.spec[slot].j = eos;
+            L.spec[slot].sel = 1;
+        } else {  // beyond the list the row is flagged and finalised from its logits
+            clear_keep_bit(L, geo.first, eos);
         }
     }
     if (R.pen) {
@@ -1336,7 +1330,8 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     }
     __syncthreads();
     MIS_STAMP(2);
-    // specials: counts, out of the tile, their logits loaded (the loads land during pass 1)
+    // specials: counts and allowed bits (the keep bit, which only the special's own thread clears), out of the
+    // tile; the logits of the allowed ones loaded (the loads land during pass 1)
     const int ns = min(L.nspec, kSpecCap);
     if (tid == 0 && L.nspec > kSpecCap) L.flags |= kRecOverflow;
     float sx[2];
@@ -1350,9 +1345,10 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
             const int j = L.spec[i].j;
             const int n = R.pen ? count_at(L, j - geo.first) : 0;
             L.spec[i].n = n;
-            if (!L.spec[i].sel) clear_keep_bit(L, geo.first, j);
-            sx[u] = load_elem<ES>(G, R.row, j);
-            sal[u] = allowed_bit(G, R.row, j);
+            const int o = j - jb;
+            sal[u] = (L.keep[o >> 5] >> (o & 31)) & 1u;
+            clear_keep_bit(L, geo.first, j);
+            if (sal[u]) sx[u] = load_elem<ES>(G, R.row, j);
         }
     }
     __syncthreads();
