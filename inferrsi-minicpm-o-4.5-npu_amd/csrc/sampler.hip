@@ -73,7 +73,6 @@ constexpr int kCapSpecSeg = 512;                 // candidates among a slice's s
 constexpr int kSegs = kWaves + 1;                // candidate segments of a slice: 16 waves + the specials
 constexpr int kCapRow = 12288;                   // entries of the histogram path's weighted list
 constexpr int kCapCand = 6144;                   // candidates a finaliser gathers (with their masses)
-constexpr int kCapSmall = 1024;                  // a narrowed candidate set
 constexpr int kBins = 2048;                      // radix digit: 11 bits
 constexpr int kMaxSB = kWaves * kRounds;         // (wave, round) sub-blocks of a slice
 constexpr double kFx = 4398046511104.0;          // 2^42 fixed-point units of exp(q - max): V * 2^42 < 2^64
@@ -197,12 +196,6 @@ struct Hist {
     unsigned long long before;
 };
 
-struct SmallSet {
-    float q[kCapSmall];
-    uint32_t id[kCapSmall];
-    unsigned long long mass[kCapSmall];
-};
-
 constexpr int kSelBins = kBins;  // value bins of the candidate finaliser (their masses live in Hist::w)
 constexpr int kSelCap = 1024;    // elements of one bin ranked exactly; specials of a row drawn from
 
@@ -233,7 +226,6 @@ struct Lds {
     uint32_t keep[kKeepWords];
     union {
         Special spec[kSpecCap];  // slice phase
-        SmallSet sm[2];          // finaliser: narrowed candidate sets (compaction alternates between the two)
         SelScratch ss;           // finaliser: the candidate selection
     };
     double sb[kMaxSB];
@@ -676,22 +668,6 @@ __device__ __forceinline__ uint32_t range_bits(int j0, int lo, int hi) {
     const uint32_t lo_m = a <= 0 ? ~0u : (a >= 32 ? 0u : (~0u << a));
     const uint32_t hi_m = b >= 32 ? ~0u : (b <= 0 ? 0u : ((1u << b) - 1u));
     return lo_m & hi_m;
-}
-
-// Appends the lanes' (qf(), j) where pred holds to the wave's candidate segment (global); cnt is wave-uniform.
-template <class QF>
-__device__ __forceinline__ void append_cand(bool pred, QF&& qf, uint32_t j, unsigned long long* seg, int cap, int& cnt,
-                                            int& flags) {
-    const uint64_t b = ballot(pred);
-    if (b == 0ull) return;
-    const int n = __popcll(b);
-    if (cnt + n > cap) {
-        flags |= kRecOverflow;
-        cnt = cap;
-        return;
-    }
-    if (pred) seg[cnt + (int)rank_below(b)] = ((unsigned long long)j << 32) | __float_as_uint(qf());
-    cnt += n;
 }
 
 // Room in an LDS list for the lanes where pred holds (wave-aggregated); -1 where it does not.
@@ -2118,33 +2094,11 @@ __device__ __forceinline__ void fin_stream(const DevGroup& G, const Row& R, Lds&
     select_draw(G, R2, L, V, m_sel, zfull, nfin, -INFINITY, true, false, 0u, 0xffffffffu, out);
 }
 
-// Inclusive prefix over the workgroup in thread order (doubles, fixed order).
-__device__ __forceinline__ double block_incl_scan_d(double x, Red& r) {
-    double incl = wave_incl_scan(x);
-    __syncthreads();
-    if (lane_id() == 63) r.d[wave_id()] = incl;
-    __syncthreads();
-    double p[kWaves];
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) p[i] = r.d[i];
-    double off = 0.0;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) off += (i < wave_id()) ? p[i] : 0.0;
-    return off + incl;
-}
-
 // ------------------------------------------------------------------ the candidate finaliser (one wave)
 //
 // Once the candidates are in LDS (gathered by the whole workgroup, each with its mass relative to the row max), the
 // selections run on wave 0 alone: no workgroup barriers, and each instruction costs one issue slot instead of
 // sixteen.  The other waves wait at the barrier that follows.
-
-// LDS written by this wave is visible to its other lanes (wave-level ordering only: no s_barrier).
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-}
 
 __device__ __forceinline__ unsigned long long readlane_u64(unsigned long long x, int lane) {
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
@@ -2172,355 +2126,9 @@ __device__ __forceinline__ WSet wset_of(float* q, uint32_t* id, unsigned long lo
     return s;
 }
 
-// What a selection counts: kSelCount (finite values), kSelCut (mass above kth), kSelDraw (keys are ids; survivors'
-// mass relative to md).
-struct WSel {
-    int sel;
-    float kth, thr, md;
-    bool md_is_m;  // md is the row max: the stored masses serve the draw
-};
-
-// Every field is loaded unconditionally and combined with selects: a load under a divergent condition is followed
-// by its own wait, and one wave has nothing else to run meanwhile.
-__device__ __forceinline__ void wentry(const WSet& s, int i, const WSel& P, uint32_t& key, unsigned long long& w) {
-    const float q = s.q[i];
-    const uint32_t id = s.id[i];
-    const unsigned long long m = s.mass[i];
-    if (P.sel == kSelDraw) {
-        key = id & ~kSelOnlyBit;
-        const unsigned long long wm = P.md_is_m ? m : efx(q, P.md);
-        w = (!(id & kSelOnlyBit) && q >= P.thr) ? wm : 0ull;
-    } else {
-        key = ord_key(q);
-        w = P.sel == kSelCount ? (q > -INFINITY ? 1ull : 0ull) : (q > P.kth ? m : 0ull);
-    }
-}
-
-// The entries of s where pred(i) holds, copied into whichever of L.sm[0], L.sm[1] s is not (so never in place),
-// or s itself when they do not fit.  Four entries per lane per step, so that their LDS reads overlap.
-template <class Pred>
-__device__ __forceinline__ WSet wcompact(const WSet& s, Pred pred, Lds& L) {
-    const int l = lane_id();
-    const bool in0 = s.q == (const MIS_LDS float*)L.sm[0].q;
-    MIS_LDS float* dq = (MIS_LDS float*)(in0 ? L.sm[1].q : L.sm[0].q);
-    MIS_LDS uint32_t* did = (MIS_LDS uint32_t*)(in0 ? L.sm[1].id : L.sm[0].id);
-    MIS_LDS unsigned long long* dm = (MIS_LDS unsigned long long*)(in0 ? L.sm[1].mass : L.sm[0].mass);
-    int cnt = 0;
-    for (int i0 = 0; i0 < s.n; i0 += 256) {
-        bool p[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + 64 * u + l;
-            p[u] = pred(min(i, s.n - 1)) && i < s.n;  // clamped: the reads are unconditional and overlap
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) cnt += __popcll(ballot(p[u]));
-    }
-    if (cnt > kCapSmall) return s;
-    int base = 0;
-    for (int i0 = 0; i0 < s.n; i0 += 256) {
-        bool p[4];
-        float q[4];
-        uint32_t id[4];
-        unsigned long long m[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + 64 * u + l, ic = min(i, s.n - 1);
-            p[u] = pred(ic) && i < s.n;
-            q[u] = s.q[ic];
-            id[u] = s.id[ic];
-            m[u] = s.mass[ic];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const uint64_t b = ballot(p[u]);
-            if (p[u]) {
-                const int slot = base + (int)rank_below(b);
-                dq[slot] = q[u];
-                did[slot] = id[u];
-                dm[slot] = m[u];
-            }
-            base += __popcll(b);
-        }
-    }
-    wave_lds_sync();
-    WSet r;
-    r.q = dq;
-    r.id = did;
-    r.mass = dm;
-    r.n = cnt;
-    return r;
-}
-
-// f(i, valid) for i = lane, lane + 64, ... < n, four per lane per step with clamped (always valid) indices.
-template <class F>
-__device__ __forceinline__ void wave_for(int n, F f) {
-    const int l = lane_id();
-    for (int i0 = 0; i0 < n; i0 += 256) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + 64 * u + l;
-            f(min(i, n - 1), i < n);
-        }
-    }
-}
-
 template <class T>
 __device__ __forceinline__ T wave_sum(T x) {
     return wave_reduce(x, [](T a, T b) { return a + b; });
-}
-
-__device__ __forceinline__ int scan_bins256(const unsigned long long* bins, bool desc, unsigned long long T,
-                                            unsigned long long& before);
-
-// One round of a wave selection: 256 bins, lane l holding bins 4l .. 4l + 3 (scan order: descending visits bins
-// 255 .. 0, ascending 0 .. 255; bins past the range are empty).  Returns the bin where the cumulative weight
-// reaches T and the weight before it, or -1 when the total is below T.
-template <class BinOf>
-__device__ __forceinline__ int wround(const WSet& s, const WSel& P, bool desc, unsigned long long T, uint32_t klo,
-                                      uint32_t khi, uint32_t vkey, unsigned long long vw, BinOf bin_of, Lds& L,
-                                      unsigned long long& before) {
-    const int l = lane_id();
-    unsigned long long* bins = L.h.w;
-    ulonglong2* bins2 = (ulonglong2*)L.h.w;
-    bins2[2 * l] = make_ulonglong2(0ull, 0ull);
-    bins2[2 * l + 1] = make_ulonglong2(0ull, 0ull);
-    wave_lds_sync();
-    for (int i0 = 0; i0 < s.n; i0 += 256) {
-        uint32_t key[4];
-        unsigned long long w[4];
-        float q[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + 64 * u + l, ic = min(i, s.n - 1);
-            wentry(s, ic, P, key[u], w[u]);
-            q[u] = s.q[ic];
-            if (i >= s.n) w[u] = 0ull;
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (w[u] && key[u] >= klo && key[u] <= khi) atomicAdd(&bins[bin_of(key[u], q[u])], w[u]);
-    }
-    if (l == 0 && vw && vkey >= klo && vkey <= khi) atomicAdd(&bins[bin_of(vkey, key_float(vkey))], vw);
-    wave_lds_sync();
-    const int b = scan_bins256(bins, desc, T, before);
-    wave_lds_sync();  // read before the next round clears them
-    return b;
-}
-
-// The bin of 256 (lane l reads bins 4l .. 4l + 3) where the cumulative weight in scan order (descending: bins
-// 255 .. 0) reaches T, and the weight before it; -1 when the total is below T.  One wave, no synchronisation.
-__device__ __forceinline__ int scan_bins256(const unsigned long long* bins, bool desc, unsigned long long T,
-                                            unsigned long long& before) {
-    const int l = lane_id();
-    const ulonglong2* bins2 = (const ulonglong2*)bins;
-    unsigned long long v[4];
-    if (desc) {
-        const ulonglong2 hi = bins2[127 - 2 * l], lo = bins2[126 - 2 * l];
-        v[0] = hi.y;
-        v[1] = hi.x;
-        v[2] = lo.y;
-        v[3] = lo.x;
-    } else {
-        const ulonglong2 a = bins2[2 * l], b = bins2[2 * l + 1];
-        v[0] = a.x;
-        v[1] = a.y;
-        v[2] = b.x;
-        v[3] = b.y;
-    }
-    const unsigned long long sum = v[0] + v[1] + v[2] + v[3];
-    const unsigned long long incl = wave_incl_scan(sum);
-    if (readlane_u64(incl, 63) < T) return -1;
-    const unsigned long long ex = incl - sum;
-    const int ls = __ffsll((long long)ballot(ex < T && T <= incl)) - 1;
-    int t = 3;
-    unsigned long long bef = ex + v[0] + v[1] + v[2];
-    if (ex + v[0] >= T) {
-        t = 0;
-        bef = ex;
-    } else if (ex + v[0] + v[1] >= T) {
-        t = 1;
-        bef = ex + v[0];
-    } else if (ex + v[0] + v[1] + v[2] >= T) {
-        t = 2;
-        bef = ex + v[0] + v[1];
-    }
-    const int pos = 4 * ls + __builtin_amdgcn_readlane(t, ls);
-    before = readlane_u64(bef, ls);
-    return desc ? 255 - pos : pos;
-}
-
-// range_find on one wave over a candidate set: the first key (descending or ascending within [klo, khi]) at which
-// the cumulative weight, with the virtual element (vkey, vw), reaches T (T >= 1); false when the total is below T.
-// A large set of values is first binned linearly by value (monotone, so the chosen bin is a value interval; keys
-// of clustered values would pile onto a few bins and serialise the LDS atomics), narrowed to that bin's entries,
-// and then binned by key, 256 bins a round.
-__device__ __forceinline__ bool wsel(WSet s, const WSel& P, bool desc, unsigned long long T, uint32_t klo,
-                                     uint32_t khi, uint32_t vkey, unsigned long long vw, Lds& L, uint32_t& key_out,
-                                     unsigned long long& before_out) {
-    const int l = lane_id();
-    unsigned long long acc = 0ull, bef = 0ull;
-    if (P.sel != kSelDraw && s.n > 64 && khi > klo) {
-        const float qlo = key_float(klo), qhi = key_float(khi);
-        const float scale = 256.0f / (qhi - qlo);
-        if (scale > 0.0f && scale < INFINITY) {
-            auto vbin = [=](uint32_t, float q) { return min(255, (int)((q - qlo) * scale)); };
-            const int b = wround(s, P, desc, T, klo, khi, vkey, vw, vbin, L, bef);
-            if (b < 0) return false;
-            T -= bef;
-            acc += bef;
-            // the entries (and the virtual element) in bin b: their keys bound the next rounds
-            uint32_t kmin = 0xffffffffu, kmax = 0u;
-            auto in_b = [&](int i) {
-                uint32_t key;
-                unsigned long long w;
-                wentry(s, i, P, key, w);
-                return key >= klo && key <= khi && vbin(key, s.q[i]) == b;
-            };
-            wave_for(s.n, [&](int i, bool ok) {
-                const bool c = in_b(i) && ok;
-                const uint32_t k = ord_key(s.q[i]);
-                kmin = min(kmin, c ? k : 0xffffffffu);
-                kmax = max(kmax, c ? k : 0u);
-            });
-            if (l == 0 && vw && vkey >= klo && vkey <= khi && vbin(vkey, key_float(vkey)) == b) {
-                kmin = min(kmin, vkey);
-                kmax = max(kmax, vkey);
-            }
-            kmin = wave_reduce(kmin, [](uint32_t a, uint32_t c) { return min(a, c); });
-            kmax = wave_reduce(kmax, [](uint32_t a, uint32_t c) { return max(a, c); });
-            klo = kmin;
-            khi = kmax;
-            s = wcompact(s, in_b, L);
-        }
-    }
-    for (;;) {
-        const uint64_t span = (uint64_t)khi - klo + 1;
-        int sh = 0;
-        while (((span - 1) >> sh) >= 256ull) ++sh;  // every key's bin (key - klo) >> sh < 256
-        const uint32_t base = klo;
-        const int b = wround(s, P, desc, T, klo, khi, vkey, vw, [=](uint32_t k, float) { return (int)((k - base) >> sh); },
-                             L, bef);
-        if (b < 0) return false;
-        T -= bef;
-        acc += bef;
-        const uint64_t a = (uint64_t)klo + ((uint64_t)b << sh);
-        klo = (uint32_t)a;
-        khi = (uint32_t)std::min<uint64_t>((uint64_t)khi, a + (1ull << sh) - 1);
-        if (sh == 0) break;
-        if (s.n > 64 && s.q == (const MIS_LDS float*)L.a.w.q) {  // narrow the gathered set once
-            const uint32_t lo_k = klo, hi_k = khi;
-            s = wcompact(s, [&](int i) {
-                uint32_t key;
-                unsigned long long w;
-                wentry(s, i, P, key, w);
-                return key >= lo_k && key <= hi_k;
-            }, L);
-        }
-    }
-    key_out = klo;
-    before_out = acc;
-    return true;
-}
-
-// select_draw for the candidate set s on wave 0 (same selections, same checks against the gate).
-__device__ __forceinline__ bool wselect_draw(const Row& R, Lds& L, WSet s, float m_sel, double zfull_fx, float gate,
-                                             bool all_gate_inf, uint32_t klo, uint32_t khi, float u, Outcome& out) {
-    const int l = lane_id();
-    const int n_fin = s.n;
-    const bool topk = R.kk < R.V;
-    WSel P;
-    P.kth = P.thr = P.md = -INFINITY;
-    P.md_is_m = true;
-    float kth = -INFINITY;
-    unsigned long long cnt_gt = (unsigned long long)n_fin;
-    uint32_t key = 0u;
-    unsigned long long bf = 0ull;
-    if (topk) {
-        if ((unsigned long long)R.kk <= (unsigned long long)n_fin) {
-            P.sel = kSelCount;
-            wsel(s, P, true, (unsigned long long)R.kk, klo, khi, 0u, 0ull, L, key, bf);
-            kth = key_float(key);
-            cnt_gt = bf;
-            if (!(kth >= gate)) return false;
-            s = wcompact(s, [&](int i) { return s.q[i] >= kth; }, L);  // the top-k set (ties included)
-            klo = key;
-        } else if (!all_gate_inf) {
-            return false;
-        }
-    }
-    float thr = kth;
-    if (R.p_active) {
-        P.kth = kth;
-        const unsigned long long ekth = efx(kth, m_sel);
-        const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
-        double zn;
-        if (topk && !R.hf) {
-            unsigned long long a = 0ull;
-            wave_for(s.n, [&](int i, bool ok) {
-                const float q = s.q[i];
-                const unsigned long long m = s.mass[i];
-                a += (ok && q > kth) ? m : 0ull;
-            });
-            zn = (double)(wave_sum(a) + vw);
-        } else {
-            zn = zfull_fx;
-        }
-        const double pt = ceil((double)R.top_p * zn);
-        const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
-        const uint32_t kthkey = ord_key(kth);
-        P.sel = kSelCut;
-        const bool found = wsel(s, P, true, T, (kth > -INFINITY) ? max(klo, kthkey) : klo, khi, kthkey, vw, L, key, bf);
-        float thr_p;
-        if (found) {
-            thr_p = key_float(key);
-        } else {
-            if (!topk) return false;  // the nucleus reaches below the candidates
-            thr_p = kth;
-        }
-        if (!topk && !(thr_p >= gate)) return false;
-        float vmk = m_sel;
-        if (R.min_keep_eff >= 2) {
-            if ((unsigned long long)R.min_keep_eff > (unsigned long long)n_fin) {
-                vmk = -INFINITY;
-            } else {
-                P.sel = kSelCount;
-                wsel(s, P, true, (unsigned long long)R.min_keep_eff, klo, khi, 0u, 0ull, L, key, bf);
-                vmk = key_float(key);
-                if (!(vmk >= gate)) return false;
-            }
-        }
-        thr = fminf(thr_p, vmk);
-        if (topk) thr = fmaxf(thr, kth);
-    }
-    // survivors: drawable, finite, q >= thr
-    s = wcompact(s, [&](int i) { return !(s.id[i] & kSelOnlyBit) && s.q[i] >= thr && s.q[i] > -INFINITY; }, L);
-    float md = -INFINITY;
-    wave_for(s.n, [&](int i, bool ok) {
-        const float q = s.q[i];
-        const uint32_t id = s.id[i];
-        md = fmaxf(md, (ok && !(id & kSelOnlyBit) && q >= thr) ? q : -INFINITY);
-    });
-    md = wave_reduce(md, [](float a, float b) { return fmaxf(a, b); });
-    out.thr = thr;
-    out.mdraw = md;
-    out.token = R.V - 1;
-    if (!(md > -INFINITY)) return true;
-    P.sel = kSelDraw;
-    P.thr = thr;
-    P.md = md;
-    P.md_is_m = md == m_sel;
-    unsigned long long zs = 0ull;
-    wave_for(s.n, [&](int i, bool ok) {
-        uint32_t k;
-        unsigned long long w;
-        wentry(s, i, P, k, w);
-        zs += ok ? w : 0ull;
-    });
-    zs = wave_sum(zs);
-    const unsigned long long T = (unsigned long long)floor((double)u * (double)zs) + 1ull;
-    if (zs > 0ull && wsel(s, P, false, T, 0u, (uint32_t)(R.V - 1), 0u, 0ull, L, key, bf)) out.token = (int64_t)key;
-    return true;
 }
 
 // ------------------------------------------------------------------ small candidate sets: sorted in registers
@@ -2708,409 +2316,6 @@ __device__ __forceinline__ bool wsort_select_draw(const Row& R, const WSet& s, f
         }
         carry = readlane_u64(incl, 63);
     }
-    return true;
-}
-
-// The draw over a set of survivors (drawable, q >= thr; 1 <= n <= 64 P) on wave 0: md, their masses relative to
-// it, and the inverse CDF in token order after a sort by id.
-template <int P>
-__device__ __forceinline__ void wsurv_draw(const WSet& sv, float m_sel, float u, Outcome& out) {
-    const int l = lane_id();
-    const int n = sv.n;
-    float q[P];
-    uint32_t id[P];
-    unsigned long long m[P];
-    float md = -INFINITY;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const int i = p * 64 + l, ic = min(i, n - 1);
-        q[p] = i < n ? sv.q[ic] : -INFINITY;
-        id[p] = sv.id[ic];
-        m[p] = sv.mass[ic];
-        md = fmaxf(md, q[p]);
-    }
-    md = wave_reduce(md, [](float a, float b) { return fmaxf(a, b); });
-    out.mdraw = md;
-    const bool md_is_m = md == m_sel;
-    unsigned long long zs = 0ull, v[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const bool in = q[p] > -INFINITY;
-        const unsigned long long m2 = in ? (md_is_m ? m[p] : efx(q[p], md)) : 0ull;
-        zs += m2;
-        v[p] = in ? (((unsigned long long)(id[p] & ~kSelOnlyBit) << 43) | m2) : ~0ull;
-    }
-    zs = wave_sum(zs);
-    if (zs == 0ull) return;
-    const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
-    wave_bitonic<P>(v);
-    unsigned long long carry = 0ull;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-        const unsigned long long w = v[p] == ~0ull ? 0ull : (v[p] & ((1ull << 43) - 1ull));
-        const unsigned long long incl = wave_incl_scan(w) + carry;
-        const uint64_t hit = ballot(v[p] != ~0ull && incl >= T2);
-        if (hit) {
-            out.token = (int64_t)(readlane_u64(v[p], __ffsll((long long)hit) - 1) >> 43);
-            return;
-        }
-        carry = readlane_u64(incl, 63);
-    }
-}
-
-// range_find over a large candidate set by the whole workgroup (every thread calls it).  Rounds of 256 bins, the
-// first by value (then later rounds keep only that bin's entries), the rest by key; each round takes one barrier:
-// every wave scans the bins itself, and the bins of consecutive rounds rotate over three buffers, so that a buffer
-// is cleared only once every wave has scanned it.
-__device__ __forceinline__ bool bsel(const WSet& s, const WSel& P, bool desc, unsigned long long T, uint32_t klo,
-                                     uint32_t khi, uint32_t vkey, unsigned long long vw, Lds& L, uint32_t& key_out,
-                                     unsigned long long& before_out) {
-    const int tid = threadIdx.x;
-    unsigned long long* buf = L.h.w;  // 3 x 256 bins
-    __syncthreads();                   // the previous selection's scans are done
-    if (tid < 256) buf[tid] = 0ull;
-    __syncthreads();
-    float qlo = 0.0f, scale = 0.0f;
-    bool value_round = false;
-    if (P.sel != kSelDraw && khi > klo) {
-        qlo = key_float(klo);
-        scale = 256.0f / (key_float(khi) - qlo);
-        value_round = scale > 0.0f && scale < INFINITY;
-    }
-    auto vbin = [&](float q) { return min(255, (int)((q - qlo) * scale)); };
-    int vsel = -1;  // after the value round: the bin every counted entry must fall in
-    unsigned long long acc = 0ull;
-    for (int r = 0;; ++r) {
-        unsigned long long* cur = buf + 256 * (r % 3);
-        unsigned long long* nxt = buf + 256 * ((r + 1) % 3);
-        int sh = 0;
-        if (!value_round) {
-            const uint64_t span = (uint64_t)khi - klo + 1;
-            while (((span - 1) >> sh) >= 256ull) ++sh;
-        }
-        for (int i = tid; i < s.n; i += kThreads) {
-            uint32_t key;
-            unsigned long long w;
-            wentry(s, i, P, key, w);
-            const float q = s.q[i];
-            const bool in = w && key >= klo && key <= khi && (vsel < 0 || vbin(q) == vsel);
-            if (in) atomicAdd(&cur[value_round ? vbin(q) : (int)((key - klo) >> sh)], w);
-        }
-        if (tid == 0 && vw && vkey >= klo && vkey <= khi) {
-            const float vq = key_float(vkey);
-            if (vsel < 0 || vbin(vq) == vsel) atomicAdd(&cur[value_round ? vbin(vq) : (int)((vkey - klo) >> sh)], vw);
-        }
-        if (tid < 256) nxt[tid] = 0ull;
-        __syncthreads();
-        unsigned long long bef = 0ull;
-        const int b = scan_bins256(cur, desc, T, bef);
-        if (b < 0) return false;
-        T -= bef;
-        acc += bef;
-        if (value_round) {
-            // keys of the bin's values, widened by a bin on each side (membership is tested by the bin itself)
-            vsel = b;
-            value_round = false;
-            const uint32_t a = ord_key(qlo + (float)(b - 1) / scale), z = ord_key(qlo + (float)(b + 2) / scale);
-            klo = max(klo, a);
-            khi = min(khi, z);
-            continue;
-        }
-        const uint64_t a = (uint64_t)klo + ((uint64_t)b << sh);
-        klo = (uint32_t)a;
-        khi = (uint32_t)std::min<uint64_t>((uint64_t)khi, a + (1ull << sh) - 1);
-        if (sh == 0) break;
-    }
-    key_out = klo;
-    before_out = acc;
-    return true;
-}
-
-// select_draw for a large candidate set by the whole workgroup (every thread calls it; the result is in out on
-// every thread).  The survivors are compacted; up to 256 of them are drawn by wave 0 with a sort.
-__device__ __forceinline__ bool bselect_draw(const Row& R, Lds& L, const WSet& s, float m_sel, double zfull_fx,
-                                             float gate, bool all_gate_inf, uint32_t klo, uint32_t khi, float u,
-                                             Outcome& out) {
-    const int tid = threadIdx.x;
-    const int n_fin = s.n;
-    const bool topk = R.kk < R.V;
-    WSel P;
-    P.kth = P.thr = P.md = -INFINITY;
-    P.md_is_m = true;
-    float kth = -INFINITY;
-    unsigned long long cnt_gt = (unsigned long long)n_fin;
-    uint32_t key = 0u;
-    unsigned long long bf = 0ull;
-    if (topk) {
-        if ((unsigned long long)R.kk <= (unsigned long long)n_fin) {
-            P.sel = kSelCount;
-            bsel(s, P, true, (unsigned long long)R.kk, klo, khi, 0u, 0ull, L, key, bf);
-            kth = key_float(key);
-            cnt_gt = bf;
-            if (!(kth >= gate)) return false;
-            klo = key;
-        } else if (!all_gate_inf) {
-            return false;
-        }
-    }
-    float thr = kth;
-    if (R.p_active) {
-        P.kth = kth;
-        const unsigned long long ekth = efx(kth, m_sel);
-        const unsigned long long vw = (topk && kth > -INFINITY) ? ((unsigned long long)R.kk - cnt_gt) * ekth : 0ull;
-        double zn;
-        if (topk && !R.hf) {
-            unsigned long long a = 0ull;
-            for (int i = tid; i < s.n; i += kThreads) {
-                const float q = s.q[i];
-                const unsigned long long m = s.mass[i];
-                a += q > kth ? m : 0ull;
-            }
-            zn = (double)(block_sum_u(a, L.red) + vw);
-        } else {
-            zn = zfull_fx;
-        }
-        const double pt = ceil((double)R.top_p * zn);
-        const unsigned long long T = pt < 1.0 ? 1ull : (unsigned long long)pt;
-        const uint32_t kthkey = ord_key(kth);
-        P.sel = kSelCut;
-        const bool found = bsel(s, P, true, T, (kth > -INFINITY) ? max(klo, kthkey) : klo, khi, kthkey, vw, L, key, bf);
-        float thr_p;
-        if (found) {
-            thr_p = key_float(key);
-        } else {
-            if (!topk) return false;
-            thr_p = kth;
-        }
-        if (!topk && !(thr_p >= gate)) return false;
-        float vmk = m_sel;
-        if (R.min_keep_eff >= 2) {
-            if ((unsigned long long)R.min_keep_eff > (unsigned long long)n_fin) {
-                vmk = -INFINITY;
-            } else {
-                P.sel = kSelCount;
-                bsel(s, P, true, (unsigned long long)R.min_keep_eff, klo, khi, 0u, 0ull, L, key, bf);
-                vmk = key_float(key);
-                if (!(vmk >= gate)) return false;
-            }
-        }
-        thr = fminf(thr_p, vmk);
-        if (topk) thr = fmaxf(thr, kth);
-    }
-    // survivors: drawable, q >= thr, compacted into L.sm[0] when they fit
-    if (tid == 0) L.scnt = 0;
-    __syncthreads();
-    SmallSet& d = L.sm[0];
-    for (int i0 = 0; i0 < s.n; i0 += kThreads) {
-        const int i = min(i0 + tid, s.n - 1);
-        const float q = s.q[i];
-        const uint32_t id = s.id[i];
-        const bool sv = i0 + tid < s.n && !(id & kSelOnlyBit) && q >= thr && q > -INFINITY;
-        const int slot = lds_reserve(sv, &L.scnt);
-        if (sv && slot < kCapSmall) {
-            d.q[slot] = q;
-            d.id[slot] = id;
-            d.mass[slot] = s.mass[i];
-        }
-    }
-    __syncthreads();
-    const int ns = L.scnt;
-    out.thr = thr;
-    out.mdraw = -INFINITY;
-    out.token = R.V - 1;
-    if (ns == 0) return true;
-    if (ns <= 256) {
-        const WSet sv = wset_of(d.q, d.id, d.mass, ns);
-        if (wave_id() == 0) {
-            Outcome o = out;
-            if (ns <= 64)
-                wsurv_draw<1>(sv, m_sel, u, o);
-            else if (ns <= 128)
-                wsurv_draw<2>(sv, m_sel, u, o);
-            else
-                wsurv_draw<4>(sv, m_sel, u, o);
-            if (lane_id() == 0) {
-                L.fscratch[3] = o.mdraw;
-                L.uscratch[1] = (unsigned long long)o.token;
-            }
-        }
-        __syncthreads();
-        out.mdraw = L.fscratch[3];
-        out.token = (int64_t)L.uscratch[1];
-        return true;
-    }
-    // many survivors: the block finds md, their sum and the draw over the whole set
-    float md = -INFINITY;
-    for (int i = tid; i < s.n; i += kThreads) {
-        const float q = s.q[i];
-        const uint32_t id = s.id[i];
-        if (!(id & kSelOnlyBit) && q >= thr) md = fmaxf(md, q);
-    }
-    md = block_max_f(md, L.red);
-    out.mdraw = md;
-    P.sel = kSelDraw;
-    P.thr = thr;
-    P.md = md;
-    P.md_is_m = md == m_sel;
-    unsigned long long zs = 0ull;
-    for (int i = tid; i < s.n; i += kThreads) {
-        uint32_t k;
-        unsigned long long w;
-        wentry(s, i, P, k, w);
-        zs += w;
-    }
-    zs = block_sum_u(zs, L.red);
-    const unsigned long long T2 = (unsigned long long)floor((double)u * (double)zs) + 1ull;
-    if (zs > 0ull && bsel(s, P, false, T2, 0u, (uint32_t)(R.V - 1), 0u, 0ull, L, key, bf)) out.token = (int64_t)key;
-    return true;
-}
-
-// Candidate rows: every slice's candidates gathered into LDS (the whole workgroup), then selected and drawn on
-// wave 0.  False: the histogram path or streaming instead.
-__device__ __forceinline__ bool fin_cands(const DevGroup& G, const Row& R, Lds& L, Outcome& out) {
-    const int S = R.S, tid = threadIdx.x, w = wave_id(), l = lane_id();
-    const int nseg = S * kSegs;
-    if (w == 0) {
-        // records (lane s: slice s) and segment counts (lane l: segments [l * per, (l + 1) * per))
-        const float u = row_uniform(G, R);
-        float mq = -INFINITY, gt = -INFINITY, mr = -INFINITY;
-        double zz = 0.0, zcc = 0.0;
-        int over = 0, notinf = 0;
-        if (l < S) {
-            const SliceRec* rec = (const SliceRec*)rec_base(G, R.row, l);
-            mq = pub_ld(&rec->mq);
-            gt = pub_ld(&rec->gate);
-            mr = pub_ld(&rec->mref);
-            zz = pub_ld(&rec->z);
-            zcc = pub_ld(&rec->zc);
-            const int fl = pub_ld(&rec->flags);
-            over = (fl & kRecOverflow) ? 1 : 0;
-            notinf = (fl & kRecGateInf) ? 0 : 1;
-        }
-        const int per = (nseg + 63) >> 6;
-        int c[kSegs];
-        int mine = 0;
-#pragma unroll
-        for (int t = 0; t < kSegs; ++t) {
-            const int i = l * per + t;
-            c[t] = (t < per && i < nseg) ? pub_ld(&((const SliceRec*)rec_base(G, R.row, i / kSegs))->ncand[i % kSegs]) : 0;
-            mine += c[t];
-        }
-        const float m_sel = wave_reduce(mq, [](float a, float b) { return fmaxf(a, b); });
-        const float gate = wave_reduce(gt, [](float a, float b) { return fmaxf(a, b); });
-        const int anyover = wave_reduce(over, [](int a, int b) { return max(a, b); });
-        const int anyfin = wave_reduce(notinf, [](int a, int b) { return max(a, b); });
-        double zs = 0.0, zcs = 0.0;
-        if (R.needz) {
-            const double sc = (mr > -INFINITY && m_sel > -INFINITY) ? exp((double)mr - (double)m_sel) : 0.0;
-            zs = wave_sum(zz * sc);
-            zcs = wave_sum(zcc * sc);
-        }
-        // a top-p row without top-k whose candidates weigh clearly less than top_p of the row cannot be cut among
-        // them: straight to the slices' histograms
-        const int short_mass = (R.mode == kNucleus && R.p_active && zcs < (double)R.top_p * zs * (1.0 - 1e-6)) ? 1 : 0;
-        const int incl = wave_incl_scan(mine);
-        int o = incl - mine;
-#pragma unroll
-        for (int t = 0; t < kSegs; ++t) {
-            const int i = l * per + t;
-            if (t < per && i < nseg) L.segoff[i] = o;
-            o += c[t];
-        }
-        if (l == 0) {
-            const int n = __builtin_amdgcn_readlane(incl, 63);
-            L.segoff[nseg] = n;
-            L.fscratch[0] = m_sel;
-            L.fscratch[1] = gate;
-            L.fscratch[2] = u;
-            L.dscratch[0] = zs;
-            L.token = anyover | short_mass;
-            L.is_last = anyfin;
-            L.uscratch[0] = 0xffffffffull;  // min key, max key of the candidates (below)
-            L.uscratch[1] = 0ull;
-        }
-    }
-    __syncthreads();
-    const int n = L.segoff[nseg];
-    MIS_STAMP(26);
-    if (L.token || n > kCapCand) return false;
-    const float m_sel = L.fscratch[0];
-    // gather, with each candidate's mass relative to the row max: four loads per thread issued together
-    uint32_t kmin = 0xffffffffu, kmax = 0u;
-    for (int i0 = 0; i0 < n; i0 += 4 * kThreads) {
-        unsigned long long v[4];
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            const int i = i0 + u4 * kThreads + tid;
-            v[u4] = 0ull;
-            if (i0 + u4 * kThreads >= n) continue;  // the whole batch is past the end
-            int lo = 0, hi = nseg;  // segment: segoff[lo] <= i < segoff[lo + 1]
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (L.segoff[mid] <= i)
-                    lo = mid;
-                else
-                    hi = mid;
-            }
-            const int s = lo / kSegs, sg = lo % kSegs;
-            const unsigned long long* seg =
-                (const unsigned long long*)(rec_base(G, R.row, s) + kRecCandOff) + (int64_t)sg * kCapWave;
-            if (i < n) v[u4] = pub_ld(seg + (i - L.segoff[lo]));
-        }
-#pragma unroll
-        for (int u4 = 0; u4 < 4; ++u4) {
-            const int i = i0 + u4 * kThreads + tid;
-            if (i >= n) continue;
-            const float q = __uint_as_float((uint32_t)v[u4]);
-            L.a.w.q[i] = q;
-            L.a.w.id[i] = (uint32_t)(v[u4] >> 32);
-            L.a.w.mass[i] = efx(q, m_sel);
-            const uint32_t k = ord_key(q);
-            kmin = min(kmin, k);
-            kmax = max(kmax, k);
-        }
-    }
-    kmin = wave_reduce(kmin, [](uint32_t a, uint32_t b) { return min(a, b); });
-    kmax = wave_reduce(kmax, [](uint32_t a, uint32_t b) { return max(a, b); });
-    if (l == 0 && n) {
-        atomicMin((unsigned long long*)&L.uscratch[0], (unsigned long long)kmin);
-        atomicMax((unsigned long long*)&L.uscratch[1], (unsigned long long)kmax);
-    }
-    __syncthreads();
-    MIS_STAMP(27);
-    const uint32_t klo = n ? (uint32_t)L.uscratch[0] : 0u, khi = n ? (uint32_t)L.uscratch[1] : 0u;
-    if (n > 256) {  // a large set: the whole workgroup selects
-        const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
-        return bselect_draw(R, L, s, m_sel, L.dscratch[0] * kFx, L.fscratch[1], L.is_last == 0, klo, khi,
-                            L.fscratch[2], out);
-    }
-    if (w == 0) {
-        const WSet s = wset_of(L.a.w.q, L.a.w.id, L.a.w.mass, n);
-        Outcome o;
-        const double zf = L.dscratch[0] * kFx;
-        const float gate = L.fscratch[1], u = L.fscratch[2];
-        const bool ginf = L.is_last == 0;
-        bool ok;
-        if (n >= 1 && n <= 64)
-            ok = wsort_select_draw<1>(R, s, m_sel, zf, gate, ginf, u, o);
-        else if (n >= 1 && n <= 128)
-            ok = wsort_select_draw<2>(R, s, m_sel, zf, gate, ginf, u, o);
-        else if (n >= 1)
-            ok = wsort_select_draw<4>(R, s, m_sel, zf, gate, ginf, u, o);
-        else
-            ok = wselect_draw(R, L, s, m_sel, zf, gate, ginf, klo, khi, u, o);
-        if (l == 0) {
-            L.token = ok ? 1 : 0;
-            L.fscratch[3] = o.thr;
-            L.dscratch[1] = o.mdraw;
-            L.uscratch[0] = (unsigned long long)o.token;
-        }
-    }
-    __syncthreads();
-    if (!L.token) return false;
-    out.thr = L.fscratch[3];
-    out.mdraw = (float)L.dscratch[1];
-    out.token = (int64_t)L.uscratch[0];
     return true;
 }
 
