@@ -242,6 +242,42 @@ def test_histories_with_more_distinct_ids_than_a_slice_lists():
     assert paths["stream"] == rows
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_greedy_ties_take_the_first_index(dtype):
+    """Greedy rows whose maximum is tied: inside one 16-byte chunk, across chunks and slices, against a masked
+    element, and between a penalised history id and a plain element (either one first); the first index wins."""
+    print(f"[gpu] greedy ties {dtype}", flush=True)
+    v = W.THINKER_V if dtype == "bf16" else V
+    rows = 7
+    gen = torch.Generator().manual_seed(83)
+    x = torch.randn(rows, v, generator=gen) * 0.5
+    p, q = 4096, v - 9
+    x[0] = 0.0
+    x[1, [p, p + 3, q]] = 5.0
+    x[2, [p, p + 1]] = 5.0
+    x[3, [q, p + 8]] = 5.0
+    x[4, [v - 1, q]] = 5.0
+    x[5, p], x[5, p + 2] = 6.25, 5.0  # 6.25 / 1.25 = 5 exactly: the history id ties with the later plain element
+    x[6, p], x[6, p + 2] = 5.0, 6.25  # ... and with the earlier one
+    x = x.to(torch.bfloat16) if dtype == "bf16" else x
+    allowed = torch.ones(rows, v, dtype=torch.bool)
+    allowed[2, p] = False
+    hist = torch.full((rows, 4), -1, dtype=torch.int32)
+    hist[5, 0], hist[6, 0] = p, p + 2
+    one = lambda val, dt=torch.float32: torch.full((rows,), val, dtype=dt)  # noqa: E731
+    words = W.pack_allowed(allowed)
+    ref_rows = ext.Rows(logits=x, temperature=one(0.0), top_k=one(0, torch.int32), top_p=one(1.0),
+                        repetition=one(1.25), presence=one(0.0), frequency=one(0.0), history=hist, mask=words,
+                        seeds=one(1, torch.int64), steps=one(1, torch.int64))
+    g = G.RowGroup(x.to(DEV), temperature=0.0, repetition=1.25, history=hist.to(DEV), allowed=words.to(DEV),
+                   seeds=one(1, torch.int64).to(DEV), steps=one(1, torch.int64).to(DEV), processed=True, probs=True)
+    G.launch([g])
+    torch.cuda.synchronize()
+    ref = ext.sample_rows(ref_rows)
+    compare_group(f"greedy_ties_{dtype}", g.tokens, g.processed, g.probs, ref, ref_rows, prob_rtol=2e-3)
+    assert g.tokens.cpu().tolist() == [0, p, p + 1, p + 8, q, p, p]
+
+
 def test_thinker_greedy_is_first_argmax_at_full_size():
     wl = W.thinker_b64().to(DEV)
     x = wl.logits.clone()
