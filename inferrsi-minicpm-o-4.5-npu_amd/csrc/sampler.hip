@@ -655,6 +655,44 @@ __device__ __forceinline__ void count_id(int64_t h, int first, int lo, int hi, i
     }
 }
 
+// count_id for the four preloaded ids of a thread at once: the four count increments issued together (an id outside
+// [lo, hi) adds 0 to a word of the lane-maxima histogram, a no-op, so that no increment sits under a branch), then
+// one reservation of list slots for all of the wave's first occurrences.
+__device__ __forceinline__ void count_ids4(const HistPre& P, int first, int lo, int hi, int skip_id, Lds& L) {
+    uint32_t old[4];
+    bool in[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = P.h[u];
+        in[u] = h >= lo && h < hi;
+        const int pos = in[u] ? h - first : 0;
+        uint32_t* word = in[u] ? &L.a.cnt[pos >> 1] : &L.gh[lane_id()];
+        old[u] = atomicAdd(word, in[u] ? 1u << (16 * (pos & 1)) : 0u);
+    }
+    uint64_t bal[4];
+    int total = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int h = P.h[u];
+        const uint32_t prev = (old[u] >> (16 * ((h - first) & 1))) & 0xffffu;
+        bal[u] = ballot(in[u] && prev == 0u && h != skip_id);
+        total += __popcll(bal[u]);
+    }
+    if (total == 0) return;
+    int base = 0;
+    if (lane_id() == 0) base = atomicAdd(&L.nspec, total);
+    base = __builtin_amdgcn_readfirstlane(base);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int slot = base + (int)rank_below(bal[u]);
+        if (((bal[u] >> lane_id()) & 1ull) && slot < kSpecCap) {
+            L.spec[slot].j = P.h[u];
+            L.spec[slot].sel = 0;
+        }
+        base += __popcll(bal[u]);
+    }
+}
+
 // The row's allowed word for keep word k of a slice whose keep words start at element jb (~0 without a mask).
 __device__ __forceinline__ uint32_t mask_word(const DevGroup& G, int row, int jb, int k, int nkw) {
     if (k >= nkw) return 0u;
@@ -1291,8 +1329,7 @@ __device__ __forceinline__ int run(const KernelArgs& A, const DevGroup& G, int g
     }
     if (R.pen) {
         const int skip = eos_here ? eos : -1;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) count_id(hp.h[u], geo.first, lo, hi, skip, L);
+        count_ids4(hp, geo.first, lo, hi, skip, L);
         if (G.hist_len > 4 * kThreads) {
             const char* hrow = hist_row(G, R.row);
             for (int b = 4 * kThreads; b < G.hist_len; b += kThreads) {
